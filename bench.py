@@ -1,0 +1,296 @@
+#!/usr/bin/env python3
+"""Benchmark: fused GDN decode step with INT8 state + packed-INT4 EF residual.
+
+Workload ("C3", at its headline batch): one
+single-layer decode step at batch 64 over 32 value heads (H = HV = 32) with
+K = V = 128, int8 per-V-row state, packed int4 residual with a per-head
+scale, fp32 activations, vLLM paged layout, in place through
+``quantized_gated_delta_rule_packed_decode`` (one kernel launch per step).
+
+Synthetic data of the config's distributions: alpha = exp(g),
+g ~ U(log 0.9, log 0.995) per (request, head), beta = sigmoid(U(-2, 2)); q, k
+L2-normalised N(0,1) (normalised on the host, kernel flag off, scale 1.0);
+v ~ N(0,1). The gates reach the kernel as A_log = 0, dt_bias = 0,
+a = log(expm1(-g)), b = logit(beta). The initial state is 64 fp32 warm-up
+steps from zero (on the GPU, fp32 state arm), then quantized into the pool.
+
+Each step takes the next group of 64 slots of a 1025-slot pool (about 0.8 GB,
+larger than the 256 MB Infinity Cache), so state reads come from HBM as they
+do when 24 layers share the cache between two steps of one layer.
+
+Prints ONE JSON line (rank 0). ``value`` is algorithmic GB/s over the timed
+steps; ``ms_per_step`` is the device time per step from HIP events on the
+launch stream.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+if HERE not in sys.path:
+    sys.path.insert(0, HERE)
+
+from carrykernel_amd.vllm_integration import quantized_packed_decode as qpd  # noqa: E402
+
+HBM_PEAK_GBPS = 8000.0
+H = HV = 32
+K = V = 128
+
+
+def algorithmic_bytes(B, H, HV, K, V, resid_fmt, per_head, act_bytes=4):
+    """Unique bytes read + written by one step.
+
+    Per (request, value-head): state codes 2*K*V; residual 2*K*V (int8) or
+    K*V (int4); state scale 2*4*V; residual scale 2*4*V (per row) or 2*4
+    (per head); v and o 2*act*V; the two gate inputs a, b 2*act. Per
+    (request, QK head): q and k 2*act*K. Per request: the 4-byte slot id.
+    """
+    resid = 2 * K * V if resid_fmt == qpd.RESID_INT8 else K * V
+    rscale = 2 * 4 if per_head else 2 * 4 * V
+    per_vhead = 2 * K * V + resid + 2 * 4 * V + rscale + 2 * act_bytes * V + 2 * act_bytes
+    per_qkhead = 2 * act_bytes * K
+    return B * (HV * per_vhead + H * per_qkhead + 4)
+
+
+def bf16_state_bytes(B, H, HV, K, V, act_bytes=4):
+    """Same step with vLLM's default bf16 state (the comparison arm)."""
+    per_vhead = 2 * 2 * K * V + 2 * act_bytes * V + 2 * act_bytes
+    return B * (HV * per_vhead + H * 2 * act_bytes * K + 4)
+
+
+def make_step_inputs(B, n_sets, device, seed):
+    """Synthetic activations in the config's distributions (see module doc)."""
+    g = torch.Generator().manual_seed(seed)
+    sets = []
+    for _ in range(n_sets):
+        q = torch.randn(B, H, K, generator=g)
+        k = torch.randn(B, H, K, generator=g)
+        q = q / q.norm(dim=-1, keepdim=True)
+        k = k / k.norm(dim=-1, keepdim=True)
+        v = torch.randn(B, HV, V, generator=g)
+        lg = torch.empty(B, HV).uniform_(math.log(0.9), math.log(0.995), generator=g)
+        a = torch.log(torch.expm1(-lg))
+        b = torch.empty(B, HV).uniform_(-2.0, 2.0, generator=g)
+        mixed = torch.cat([q.reshape(B, -1), k.reshape(B, -1), v.reshape(B, -1)], dim=1).contiguous()
+        sets.append(tuple(x.to(device) for x in (mixed, a.contiguous(), b.contiguous())))
+    A_log = torch.zeros(HV, device=device)
+    dt_bias = torch.zeros(HV, device=device)
+    return sets, A_log, dt_bias
+
+
+def warm_state(S, device, seed):
+    """64 fp32 warm-up steps from zero on slots 1..S-1, then quantize."""
+    from carrykernel_amd import _native
+    state = torch.zeros(S, HV, V, K, device=device)
+    sets, A_log, dt_bias = make_step_inputs(S - 1, 4, device, seed + 17)
+    idx = torch.arange(1, S, dtype=torch.int32, device=device)
+    out = torch.empty(S - 1, 1, HV, V, device=device)
+    L = _native.lib()
+    for t in range(64):
+        mixed, a, b = sets[t % len(sets)]
+        st = L.ck_gdn_packed_decode_float_state(
+            mixed.data_ptr(), 0, mixed.stride(0), a.data_ptr(), 0, a.stride(0), b.data_ptr(), 0, b.stride(0),
+            A_log.data_ptr(), 0, dt_bias.data_ptr(), 0, 1.0, state.data_ptr(), 0, state.stride(0),
+            out.data_ptr(), 0, idx.data_ptr(), 1, S, S - 1, H, HV, K, V, 0,
+            _native.stream_handle(state.device))
+        _native.check(st, "warm-up")
+    return state
+
+
+def cpu_baseline(B, resid_fmt, per_head, seconds=12.0):
+    """The CPU oracle (C, OpenMP over (request, head)) on the same workload
+    shape, timed on this host for about `seconds`."""
+    import numpy as np
+    import oracle
+    nthreads = len(os.sched_getaffinity(0))
+    nthreads = min(nthreads, 16)
+    S = B + 1
+    rng = np.random.default_rng(0)
+    h0 = (rng.standard_normal((S, HV, V, K)) * 0.1).astype(np.float32)
+    sc, ss = oracle.quantize_rows(h0)
+    rc = np.zeros((S, HV, V, K // 2 if resid_fmt == qpd.RESID_INT4 else K), np.int8)
+    rs = np.zeros((S, HV) if per_head else (S, HV, V), np.float32)
+    sets, A_log, dt_bias = make_step_inputs(B, 2, "cpu", 5)
+    idx = np.arange(1, B + 1, dtype=np.int32)
+    steps = 0
+    t0 = time.perf_counter()
+    while True:
+        mixed, a, b = sets[steps % 2]
+        oracle.packed_decode(mixed.numpy(), a.numpy(), b.numpy(), A_log.numpy(), dt_bias.numpy(), 1.0,
+                             sc, ss, rc, rs, idx, H, resid_fmt=resid_fmt, per_head=per_head,
+                             nthreads=nthreads)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or steps >= 200:
+            break
+    us = el / steps * 1e6
+    gbps = algorithmic_bytes(B, H, HV, K, V, resid_fmt, per_head) / (us * 1e-6) / 1e9
+    return {"value": round(gbps, 3), "unit": "GB/s", "us_per_step": round(us, 1), "cores": nthreads,
+            "kind": "port",
+            "sample": f"{steps} steps of the B={B} workload through the C oracle (oracle/gdn_oracle.c, "
+                      f"OpenMP, {nthreads} threads), {el:.1f} s"}
+
+
+class Timer:
+    """HIP events on the launch stream (torch's current stream)."""
+
+    def __init__(self, device):
+        self.s = torch.cuda.Event(enable_timing=True)
+        self.e = torch.cuda.Event(enable_timing=True)
+        self.stream = torch.cuda.current_stream(device)
+
+    def start(self):
+        self.s.record(self.stream)
+
+    def stop_ms(self):
+        self.e.record(self.stream)
+        self.e.synchronize()
+        return self.s.elapsed_time(self.e)
+
+
+def run_config(device, B, resid_fmt, per_head, steps, warmup, groups, quant_mode="fast", seed=0):
+    """Returns (device ms per step from a replayed graph, host-inclusive ms per
+    eager call). The graph holds one step per slot group."""
+    S = B * groups + 1
+    state = warm_state(S, device, seed)
+    pool = qpd.init_quantized_state(S, HV, V, K, device, h0=state, resid_fmt=resid_fmt,
+                                    per_head_resid_scale=per_head)
+    del state
+    torch.cuda.empty_cache()
+    sets, A_log, dt_bias = make_step_inputs(B, 8, device, seed + 1)
+    perm = torch.randperm(S - 1, generator=torch.Generator().manual_seed(seed)) + 1
+    idx_groups = [perm[i * B:(i + 1) * B].to(torch.int32).to(device) for i in range(groups)]
+    out = torch.empty(B, 1, HV, V, device=device)
+
+    def step(t):
+        mixed, a, b = sets[t % len(sets)]
+        qpd.quantized_gated_delta_rule_packed_decode(
+            mixed, a, b, A_log, dt_bias, 1.0, *pool, out, idx_groups[t % groups],
+            resid_fmt=resid_fmt, quant_mode=quant_mode)
+
+    # eager calls: host-inclusive latency per call
+    for t in range(min(warmup, 50)):
+        step(t)
+    torch.cuda.synchronize()
+    n_eager = 50
+    t0 = time.perf_counter()
+    for t in range(n_eager):
+        step(t)
+    torch.cuda.synchronize()
+    host_ms = (time.perf_counter() - t0) * 1e3 / n_eager
+
+    # graph of `groups` consecutive steps, replayed
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            for t in range(groups):
+                step(t)
+    torch.cuda.current_stream(device).wait_stream(side)
+    torch.cuda.synchronize()
+    reps_w = max(1, -(-warmup // groups))
+    reps = max(1, -(-steps // groups))
+    for _ in range(reps_w):
+        graph.replay()
+    torch.cuda.synchronize()
+    timer = Timer(device)
+    timer.start()
+    for _ in range(reps):
+        graph.replay()
+    ms = timer.stop_ms() / (reps * groups)
+    torch.cuda.synchronize()
+    if not torch.isfinite(out).all():
+        raise RuntimeError("non-finite output in the timed run")
+    del graph, pool
+    torch.cuda.empty_cache()
+    return ms, host_ms
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--groups", type=int, default=16, help="disjoint slot groups rotated over")
+    ap.add_argument("--resid", choices=("int4", "int8"), default="int4")
+    ap.add_argument("--rscale", choices=("head", "row"), default="head")
+    ap.add_argument("--quant-mode", choices=("fast", "exact"), default="fast")
+    ap.add_argument("--sweep", action="store_true", help="also time B in {1, 8, 64, 256} and variants")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the decode step shards with no exchange between GPUs "
+              "(requests or value heads per GPU), so only --gpus 1 is run here.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    device = torch.device("cuda", 0)
+    resid_fmt = qpd.RESID_INT4 if args.resid == "int4" else qpd.RESID_INT8
+    per_head = args.rscale == "head"
+    B = args.batch
+
+    ms, host_ms = run_config(device, B, resid_fmt, per_head, args.steps, args.warmup, args.groups,
+                             args.quant_mode)
+    nbytes = algorithmic_bytes(B, H, HV, K, V, resid_fmt, per_head)
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    line = {
+        "metric": "GDN decode step: achieved HBM GB/s (algorithmic bytes / device time), batch 64, 1 GPU",
+        "value": round(gbps, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "us_per_step": round(ms * 1e3, 3),
+        "host_us_per_eager_call": round(host_ms * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 state / int4 residual, fp32 arithmetic",
+        "data": "synthetic (config distributions; state from 64 fp32 warm-up steps)",
+        "config": {"workload": "C3: single-layer fused decode, int8 per-V state + packed int4 EF residual "
+                               "(per-head scale), vLLM [slots,HV,V,K] layout",
+                   "batch": B, "value_heads": HV, "qk_heads": H, "K": K, "V": V,
+                   "resid": args.resid, "resid_scale": args.rscale, "quant_mode": args.quant_mode,
+                   "pool_slots": B * args.groups + 1},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "bytes_per_launch": nbytes},
+        "bytes_vs_bf16_state": round(bf16_state_bytes(B, H, HV, K, V) / nbytes, 4),
+    }
+    traffic_path = os.path.join(HERE, "profiles", "traffic_packed_decode_b64.json")
+    if os.path.exists(traffic_path):
+        with open(traffic_path) as f:
+            line["roofline"]["traffic"] = json.load(f).get("traffic_bytes_per_launch")
+    if args.sweep:
+        sweep = {}
+        for bb in (1, 8, 64, 256):
+            for fmt_name, fmt, ph in (("int4_head", qpd.RESID_INT4, True), ("int4_row", qpd.RESID_INT4, False),
+                                      ("int8_head", qpd.RESID_INT8, True), ("int8_row", qpd.RESID_INT8, False)):
+                groups = max(2, min(64, 1024 // bb))
+                m, hm = run_config(device, bb, fmt, ph, max(200, args.steps // 4), 50, groups, args.quant_mode)
+                nb = algorithmic_bytes(bb, H, HV, K, V, fmt, ph)
+                sweep[f"B{bb}_{fmt_name}"] = {"us": round(m * 1e3, 3), "host_us": round(hm * 1e3, 3),
+                                             "GBps": round(nb / (m * 1e-3) / 1e9, 1),
+                                             "frac": round(nb / (m * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+        line["sweep"] = sweep
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(B, resid_fmt, per_head, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,138 @@
+"""Loader for the gfx950 HIP library behind the C ABI (``include/carrykernel_gdn.h``).
+
+The library is linked against ``libamdhip64.so.7``. ``torch`` is imported
+first so that the dynamic loader binds the library to the HIP runtime torch
+already loaded: device pointers and ``hipStream_t`` handles taken from torch
+tensors and streams are then valid in the library.
+
+There is no CPU fallback: if the library is missing or no GPU is visible the
+entry points raise ``HipUnavailable`` (a ``RuntimeError``).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG_DIR, "lib", "libcarrykernel_gdn.so")
+
+ABI_VERSION = 1
+
+# enum ck_status
+CK_OK = 0
+CK_EINVAL = 1
+CK_EUNSUPPORTED = 2
+CK_ELAUNCH = 3
+
+# enum ck_dtype
+DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+
+# enum ck_res_fmt / ck_resid_fmt / ck_rscale_mode / ck_quant_mode
+QUANT_FAST = 0
+QUANT_EXACT = 1
+RSCALE_PER_ROW = 0
+RSCALE_PER_HEAD = 1
+
+
+class HipUnavailable(RuntimeError):
+    """The HIP library or a GPU is not available."""
+
+
+_lock = threading.Lock()
+_lib = None
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_flt = ctypes.c_float
+
+_SIGNATURES = {
+    "ck_last_error": (ctypes.c_char_p, []),
+    "ck_abi_version": (_int, []),
+    "ck_gdn_packed_decode": (_int, [
+        _vp, _int, _i64,          # mixed_qkv, dtype, stride
+        _vp, _int, _i64,          # a
+        _vp, _int, _i64,          # b
+        _vp, _int,                # A_log
+        _vp, _int,                # dt_bias
+        _flt,                     # scale
+        _vp, _i64, _vp, _i64,     # state codes / scale
+        _vp, _i64, _vp, _i64,     # resid codes / scale
+        _vp, _int,                # out
+        _vp, _i64,                # indices
+        _i64,                     # num_slots
+        _int, _int, _int, _int, _int,   # B H HV K V
+        _int, _int, _int, _int, _int,   # l2norm resid_fmt rscale_mode bits quant_mode
+        _vp]),
+    "ck_gdn_packed_decode_float_state": (_int, [
+        _vp, _int, _i64, _vp, _int, _i64, _vp, _int, _i64, _vp, _int, _vp, _int, _flt,
+        _vp, _int, _i64, _vp, _int, _vp, _i64, _i64,
+        _int, _int, _int, _int, _int, _int, _vp]),
+    "ck_gdn_quant_step": (_int, [
+        _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+        _vp, _vp, _vp, _vp, _vp,
+        _int, _int, _int, _int, _flt, _int, _int, _vp]),
+    "ck_gdn_fp32_step": (_int, [
+        _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _vp]),
+    "ck_quantize_rows": (_int, [_vp, _int, _i64, _i64, _int, _flt, _vp, _vp, _vp]),
+    "ck_quantize_cols": (_int, [_vp, _i64, _int, _int, _flt, _vp, _vp, _vp]),
+}
+
+
+def library_available() -> bool:
+    return os.path.exists(LIB_PATH)
+
+
+def lib():
+    """Load (once) and return the ctypes handle; raises HipUnavailable."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise HipUnavailable(
+                    f"{LIB_PATH} is missing: build it with `python -m carrykernel_amd.build`")
+            L = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in _SIGNATURES.items():
+                fn = getattr(L, name, None)
+                if fn is None:
+                    continue
+                fn.restype = res
+                fn.argtypes = args
+            if L.ck_abi_version() != ABI_VERSION:
+                raise HipUnavailable("libcarrykernel_gdn.so ABI version mismatch; rebuild it")
+            _lib = L
+    return _lib
+
+
+def exported_symbols() -> list[str]:
+    return list(_SIGNATURES)
+
+
+def require_gpu(t: torch.Tensor, name: str) -> None:
+    if not t.is_cuda:
+        raise HipUnavailable(
+            f"{name} is on {t.device}; the HIP kernels need GPU tensors (there is no CPU path)")
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def check(status: int, what: str) -> None:
+    if status == CK_OK:
+        return
+    msg = lib().ck_last_error().decode(errors="replace")
+    if status in (CK_EINVAL, CK_EUNSUPPORTED):
+        raise ValueError(f"{what}: {msg}")
+    raise RuntimeError(f"{what}: {msg}")
+
+
+def dtype_code(t: torch.Tensor, name: str) -> int:
+    try:
+        return DTYPE_CODES[t.dtype]
+    except KeyError:
+        raise ValueError(f"{name} must be float32, bfloat16 or float16, got {t.dtype}") from None

@@ -1,0 +1,274 @@
+"""INT8 + error-feedback recurrent state for vLLM's GDN packed decode, on MI355X.
+
+Drop-in for ``vllm_integration/quantized_packed_decode.py`` of
+tomalmog/carrykernel: same public names, constants, call signature, argument
+meaning, in-place semantics and ``ValueError`` messages
+(quantized_packed_decode.py:73-83, :242-369). The device work is a
+hand-written gfx950 HIP kernel reached through the C ABI in
+``include/carrykernel_gdn.h`` (``ck_gdn_packed_decode``).
+
+State pool per slot, per value-head (vLLM's ``[num_slots, HV, V, K]``, K
+contiguous):
+  * ``state_codes`` int8 ``[S, HV, V, K]`` and ``state_scale`` fp32 ``[S, HV, V]``
+  * ``resid_codes`` int8 ``[S, HV, V, K]`` (RESID_INT8) or packed nibbles
+    ``[S, HV, V, K/2]`` (RESID_INT4, even K in the low nibble)
+  * ``resid_scale`` fp32 ``[S, HV, V]`` (one scale per V-row, the reference's
+    layout) or ``[S, HV]`` (one scale per head; the per-head residual scale of
+    the benchmark's configs 2 and 3). The shape selects the mode.
+
+Per step (one launch): dequantize, decay, delta-rule rank-1 write, output
+read, add the carried residual, requantize with round-half-to-even, store
+codes, scales and residual in place. Slot ids <= 0 are ``NULL_BLOCK_ID``
+padding: ``out`` gets zeros and no state is touched.
+
+Differences from the reference, all additive:
+  * ``state_bits`` (default 8) sets the state code range to
+    +-(2^(bits-1) - 1) (int6 for the long-horizon config).
+  * ``quant_mode="fast"`` (default) rounds ``t * (1/s)``; ``"exact"`` rounds
+    the correctly rounded quotient ``t / s`` with op-by-op rounding.
+  * Slot ids >= num_slots make the kernel emit NaN and skip the state, where
+    the reference would access memory out of bounds.
+  * Tensors must be on a GPU; there is no CPU fallback.
+"""
+
+from __future__ import annotations
+
+import os
+
+import torch
+
+from .. import _native
+
+QMAX_INT8 = 127.0
+QMAX_INT4 = 7.0
+EPS = 1e-12
+SOFTPLUS_THRESHOLD = 20.0
+NULL_BLOCK_ID = 0
+
+RESID_INT8 = 0
+RESID_INT4 = 1
+
+HAS_HIP = _native.library_available()
+
+SUPPORTED_K = (16, 32, 64, 128, 256)
+
+_QUANT_MODES = {"fast": _native.QUANT_FAST, "exact": _native.QUANT_EXACT}
+
+# CARRYKERNEL_DEBUG=1 adds host-side checks of ssm_state_indices (range and
+# duplicate slot ids, which would race on the in-place update). They copy the
+# indices to the host, so they synchronise the stream.
+_DEBUG = os.environ.get("CARRYKERNEL_DEBUG", "0") not in ("", "0")
+
+
+def _check_indices_host(ssm_state_indices: torch.Tensor, num_slots: int) -> None:
+    ids = ssm_state_indices.detach().to("cpu").tolist()
+    live = [i for i in ids if i > NULL_BLOCK_ID]
+    if any(i >= num_slots for i in live):
+        raise ValueError(f"ssm_state_indices has slot ids >= num_slots ({num_slots})")
+    if len(set(live)) != len(live):
+        raise ValueError("ssm_state_indices has duplicate slot ids (in-place update would race)")
+
+
+def _slot_contiguous(t: torch.Tensor) -> bool:
+    """Every dim but the slot dim is densely packed (row-major)."""
+    expect = 1
+    for size, stride in zip(reversed(t.shape[1:]), reversed(t.stride()[1:])):
+        if size != 1 and stride != expect:
+            return False
+        expect *= size
+    return True
+
+
+def quantized_gated_delta_rule_packed_decode(
+    mixed_qkv: torch.Tensor,
+    a: torch.Tensor,
+    b: torch.Tensor,
+    A_log: torch.Tensor,
+    dt_bias: torch.Tensor,
+    scale: float,
+    state_codes: torch.Tensor,
+    state_scale: torch.Tensor,
+    resid_codes: torch.Tensor,
+    resid_scale: torch.Tensor,
+    out: torch.Tensor,
+    ssm_state_indices: torch.Tensor,
+    use_qk_l2norm_in_kernel: bool = False,
+    resid_fmt: int = RESID_INT8,
+    *,
+    state_bits: int = 8,
+    quant_mode: str = "fast",
+):
+    """INT8 + error-feedback drop-in for ``fused_recurrent_gated_delta_rule_packed_decode``.
+
+    Signature of quantized_packed_decode.py:242-257. Updates the four pool
+    tensors and ``out`` in place, asynchronously on the current stream, and
+    returns ``out``.
+    """
+    if not _native.library_available():
+        raise RuntimeError("The HIP library is required for the quantized packed decode "
+                           "(build it with `python -m carrykernel_amd.build`)")
+
+    # validation and messages follow quantized_packed_decode.py:268-309
+    if mixed_qkv.dim() != 2:
+        raise ValueError(f"mixed_qkv must be 2-D, got {tuple(mixed_qkv.shape)}")
+    if mixed_qkv.stride(-1) != 1:
+        raise ValueError("mixed_qkv must be contiguous in its last dimension")
+    if state_codes.dim() != 4:
+        raise ValueError(f"state_codes must be 4-D, got {tuple(state_codes.shape)}")
+    if state_codes.stride(-1) != 1:
+        raise ValueError("state_codes must be contiguous in its last dimension")
+    if state_codes.dtype != torch.int8 or resid_codes.dtype != torch.int8:
+        raise ValueError("state_codes and resid_codes must be int8 storage")
+    if resid_fmt == RESID_INT4 and resid_codes.shape[-1] * 2 != state_codes.shape[-1]:
+        raise ValueError(
+            "int4 residual must be packed two codes per byte: expected last dim "
+            f"{state_codes.shape[-1] // 2}, got {resid_codes.shape[-1]}")
+    if resid_fmt == RESID_INT8 and resid_codes.shape != state_codes.shape:
+        raise ValueError("int8 residual must have the same shape as the state")
+    if resid_fmt not in (RESID_INT8, RESID_INT4):
+        raise ValueError(f"resid_fmt must be RESID_INT8 or RESID_INT4, got {resid_fmt}")
+    if ssm_state_indices.dim() != 1:
+        raise ValueError("ssm_state_indices must be 1-D")
+    if ssm_state_indices.dtype != torch.int32:
+        raise ValueError("ssm_state_indices must be int32")
+
+    B = mixed_qkv.shape[0]
+    num_slots, HV, V, K = state_codes.shape
+    if out.shape != (B, 1, HV, V):
+        raise ValueError(f"out must be {(B, 1, HV, V)}, got {tuple(out.shape)}")
+    if not out.is_contiguous():
+        raise ValueError("out must be contiguous")
+
+    # H is inferred from the packed width, exactly as upstream does.
+    qkv_dim = mixed_qkv.shape[1]
+    qk_dim = qkv_dim - HV * V
+    if qk_dim <= 0 or qk_dim % 2 != 0:
+        raise ValueError(f"cannot infer H from mixed_qkv width {qkv_dim}")
+    H = (qk_dim // 2) // K
+    if H <= 0 or 2 * H * K != qk_dim or HV % H != 0:
+        raise ValueError(f"cannot infer H from mixed_qkv width {qkv_dim}")
+    if resid_fmt == RESID_INT4 and K % 2 != 0:
+        raise ValueError(f"int4 residual packing needs an even K, got {K}")
+    if K not in SUPPORTED_K:
+        raise ValueError(f"packed decode supports K in {SUPPORTED_K}, got K={K}")
+
+    # checks the reference leaves implicit
+    if state_scale.shape != (num_slots, HV, V) or state_scale.dtype != torch.float32:
+        raise ValueError(f"state_scale must be float32 {(num_slots, HV, V)}, "
+                         f"got {state_scale.dtype} {tuple(state_scale.shape)}")
+    if resid_scale.dtype != torch.float32:
+        raise ValueError("resid_scale must be float32")
+    if resid_scale.shape == (num_slots, HV, V):
+        rscale_mode = _native.RSCALE_PER_ROW
+    elif resid_scale.shape == (num_slots, HV):
+        rscale_mode = _native.RSCALE_PER_HEAD
+    else:
+        raise ValueError(f"resid_scale must be {(num_slots, HV, V)} (per V-row) or "
+                         f"{(num_slots, HV)} (per head), got {tuple(resid_scale.shape)}")
+    if resid_codes.shape[:3] != (num_slots, HV, V):
+        raise ValueError("resid_codes must have the state's slot, head and V dims")
+    for name, t in (("state_codes", state_codes), ("state_scale", state_scale),
+                    ("resid_codes", resid_codes), ("resid_scale", resid_scale)):
+        if not _slot_contiguous(t):
+            raise ValueError(f"{name} must be contiguous within a slot")
+    for name, t in (("a", a), ("b", b)):
+        if t.dim() != 2 or t.shape != (B, HV) or t.stride(-1) != 1:
+            raise ValueError(f"{name} must be [B, HV] = {(B, HV)} with a contiguous last dim")
+    for name, t in (("A_log", A_log), ("dt_bias", dt_bias)):
+        if t.shape != (HV,) or t.stride(0) != 1:
+            raise ValueError(f"{name} must be a contiguous [HV] = ({HV},) tensor")
+    if ssm_state_indices.shape[0] < B:
+        raise ValueError(f"ssm_state_indices must have at least B={B} entries")
+    if quant_mode not in _QUANT_MODES:
+        raise ValueError(f"quant_mode must be one of {tuple(_QUANT_MODES)}, got {quant_mode!r}")
+    if not 2 <= int(state_bits) <= 8:
+        raise ValueError(f"state_bits must be in 2..8, got {state_bits}")
+
+    dev = state_codes.device
+    tensors = (("mixed_qkv", mixed_qkv), ("a", a), ("b", b), ("A_log", A_log),
+               ("dt_bias", dt_bias), ("state_codes", state_codes), ("state_scale", state_scale),
+               ("resid_codes", resid_codes), ("resid_scale", resid_scale), ("out", out),
+               ("ssm_state_indices", ssm_state_indices))
+    for name, t in tensors:
+        _native.require_gpu(t, name)
+        if t.device != dev:
+            raise ValueError(f"{name} is on {t.device}, the state pool on {dev}")
+    if _DEBUG:
+        _check_indices_host(ssm_state_indices[:B], num_slots)
+
+    L = _native.lib()
+    status = L.ck_gdn_packed_decode(
+        mixed_qkv.data_ptr(), _native.dtype_code(mixed_qkv, "mixed_qkv"), mixed_qkv.stride(0),
+        a.data_ptr(), _native.dtype_code(a, "a"), a.stride(0),
+        b.data_ptr(), _native.dtype_code(b, "b"), b.stride(0),
+        A_log.data_ptr(), _native.dtype_code(A_log, "A_log"),
+        dt_bias.data_ptr(), _native.dtype_code(dt_bias, "dt_bias"),
+        float(scale),
+        state_codes.data_ptr(), state_codes.stride(0),
+        state_scale.data_ptr(), state_scale.stride(0),
+        resid_codes.data_ptr(), resid_codes.stride(0),
+        resid_scale.data_ptr(), resid_scale.stride(0),
+        out.data_ptr(), _native.dtype_code(out, "out"),
+        ssm_state_indices.data_ptr(), ssm_state_indices.stride(0),
+        num_slots, B, H, HV, K, V,
+        int(bool(use_qk_l2norm_in_kernel)), int(resid_fmt), rscale_mode,
+        int(state_bits), _QUANT_MODES[quant_mode],
+        _native.stream_handle(dev))
+    _native.check(status, "quantized_gated_delta_rule_packed_decode")
+    return out
+
+
+def init_quantized_state(num_slots: int, HV: int, V: int, K: int, device,
+                         h0: torch.Tensor | None = None,
+                         resid_fmt: int = RESID_INT8,
+                         *,
+                         per_head_resid_scale: bool = False,
+                         state_bits: int = 8):
+    """Allocate the quantized state pool, optionally seeding slot contents.
+
+    quantized_packed_decode.py:330-352. ``h0``, when given, is
+    ``[num_slots, HV, V, K]`` (fp32 / bf16 / fp16) and is quantized into the
+    pool on the GPU (``ck_quantize_rows``: scale = max(amax_K, eps) / qmax,
+    codes = rne(h0 / scale)); the residual starts at zero. Returns
+    ``(state_codes, state_scale, resid_codes, resid_scale)``.
+    ``per_head_resid_scale`` allocates ``resid_scale`` as ``[num_slots, HV]``.
+    """
+    device = torch.device(device)
+    if device.type != "cuda":
+        raise _native.HipUnavailable(f"the quantized pool lives on a GPU, got device {device}")
+    resid_k = K // 2 if resid_fmt == RESID_INT4 else K
+    state_codes = torch.zeros((num_slots, HV, V, K), dtype=torch.int8, device=device)
+    state_scale = torch.zeros((num_slots, HV, V), dtype=torch.float32, device=device)
+    resid_codes = torch.zeros((num_slots, HV, V, resid_k), dtype=torch.int8, device=device)
+    rs_shape = (num_slots, HV) if per_head_resid_scale else (num_slots, HV, V)
+    resid_scale = torch.zeros(rs_shape, dtype=torch.float32, device=device)
+
+    if h0 is not None:
+        if tuple(h0.shape) != (num_slots, HV, V, K):
+            raise ValueError(f"h0 must be {(num_slots, HV, V, K)}, got {tuple(h0.shape)}")
+        _native.require_gpu(h0, "h0")
+        h0 = h0.to(device).contiguous()
+        qmax = float(2 ** (int(state_bits) - 1) - 1)
+        L = _native.lib()
+        status = L.ck_quantize_rows(h0.data_ptr(), _native.dtype_code(h0, "h0"), K,
+                                    num_slots * HV * V, K, qmax,
+                                    state_codes.data_ptr(), state_scale.data_ptr(),
+                                    _native.stream_handle(device))
+        _native.check(status, "init_quantized_state")
+    return state_codes, state_scale, resid_codes, resid_scale
+
+
+def state_bytes_per_slot(HV: int, V: int, K: int, quantized: bool,
+                         base_dtype_size: int = 4, resid_fmt: int = RESID_INT8,
+                         *, per_head_resid_scale: bool = False):
+    """Bytes of recurrent state per request slot (quantized_packed_decode.py:355-369).
+
+    ``per_head_resid_scale`` counts one fp32 residual scale per head instead of
+    one per V-row.
+    """
+    if not quantized:
+        return HV * V * K * base_dtype_size
+    codes = HV * V * K
+    resid = HV * V * (K // 2 if resid_fmt == RESID_INT4 else K)
+    scales = HV * V * 4 + (HV * 4 if per_head_resid_scale else HV * V * 4)
+    return codes + resid + scales

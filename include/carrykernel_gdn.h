@@ -1,0 +1,171 @@
+/*
+ * carrykernel_gdn.h - C ABI of the MI355X (gfx950) fused Gated DeltaNet decode
+ * step with error-feedback (EF) state quantization.
+ *
+ * Every entry point takes raw device pointers, element strides and sizes, and a
+ * hipStream_t passed as void*. None allocates, none synchronises: kernels are
+ * enqueued on `stream` and the call returns. The return value is a ck_status;
+ * on failure ck_last_error() returns a message (thread-local).
+ *
+ * Reference interfaces replaced (paths relative to the tomalmog/carrykernel
+ * repository root):
+ *   ck_gdn_packed_decode      <- vllm_integration/quantized_packed_decode.py:242-327
+ *                                (host) and _quant_int8_kernel :101-239 (device)
+ *   ck_gdn_packed_decode_float_state
+ *                             <- the upstream bf16/fp32-state packed decode that
+ *                                quantized_packed_decode.py:1-7 replaces
+ *                                (invoked at modal_vllm_headtohead.py:122-125)
+ *   ck_gdn_quant_step         <- cuda/gdn_state_kernel.cu:310-348 (gdn_quant_step,
+ *                                pybind at :373-377) and statequant/kernel.py:379-408
+ *   ck_gdn_fp32_step          <- cuda/gdn_state_kernel.cu:350-371 (gdn_fp32_step)
+ *                                and statequant/kernel.py:411-433
+ *   ck_quantize_rows          <- vllm_integration/quantized_packed_decode.py:347-351
+ *                                (init_quantized_state seeding from h0)
+ *   ck_quantize_cols          <- statequant/kernel.py:99-113 (per_v_channel_quantize)
+ */
+#ifndef CARRYKERNEL_GDN_H_
+#define CARRYKERNEL_GDN_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+enum ck_status {
+  CK_OK = 0,
+  CK_EINVAL = 1,       /* bad argument (null pointer, bad size/stride/dtype)   */
+  CK_EUNSUPPORTED = 2, /* valid but not implemented here (e.g. K not in 16..256) */
+  CK_ELAUNCH = 3       /* the HIP runtime rejected the kernel launch            */
+};
+
+/* Element types of activations / outputs / float state. */
+enum ck_dtype { CK_DTYPE_F32 = 0, CK_DTYPE_BF16 = 1, CK_DTYPE_F16 = 2 };
+
+/* Residual formats of the vLLM-layout path (quantized_packed_decode.py:82-83). */
+enum ck_resid_fmt { CK_RESID_INT8 = 0, CK_RESID_INT4 = 1 };
+
+/* Residual formats of the statequant-layout path (statequant/kernel.py:60-63). */
+enum ck_res_fmt { CK_RES_FP32 = 0, CK_RES_FP16 = 1, CK_RES_FP8 = 2, CK_RES_INT8 = 3 };
+
+/* Granularity of the residual scale in the vLLM-layout path. PER_ROW is the
+ * reference's one scale per V-row (quantized_packed_decode.py:212-215);
+ * PER_HEAD is one scale per (slot, value-head), amax over the whole [V, K]
+ * tile, as configs 2/3 of the benchmark specify. */
+enum ck_rscale_mode { CK_RSCALE_PER_ROW = 0, CK_RSCALE_PER_HEAD = 1 };
+
+/* Arithmetic mode of the quantizer. FAST rounds rne(t * RN(1/s)) with one fma
+ * and forms the residual with an fma; EXACT rounds rne(RN(t / s)) (the
+ * correctly rounded quotient, as torch.round(target / scale) does) and forms
+ * the residual as RN(t - RN(code * s)). */
+enum ck_quant_mode { CK_QUANT_FAST = 0, CK_QUANT_EXACT = 1 };
+
+/* Message of the last failed call on this thread ("" after a success). */
+const char* ck_last_error(void);
+
+/* ABI version of this library (bumped on any signature change). */
+int ck_abi_version(void);
+
+/*
+ * One decode step of the vLLM-layout quantized GDN, updated in place.
+ *
+ * mixed_qkv [B, 2*H*K + HV*V] (row stride stride_qkv_tok elements, last dim
+ *   contiguous): q at i_h*K, k at H*K + i_h*K, v at 2*H*K + hv*V, with
+ *   i_h = hv / (HV / H) (grouped-query mapping).
+ * a, b [B, HV] (row strides given); A_log, dt_bias [HV].
+ * State pool, per slot contiguous [HV, V, K] int8 codes; state_scale per slot
+ *   [HV, V] fp32; resid_codes per slot [HV, V, K] int8 (CK_RESID_INT8) or
+ *   [HV, V, K/2] packed nibbles (CK_RESID_INT4: even K in the low nibble);
+ *   resid_scale per slot [HV, V] (CK_RSCALE_PER_ROW) or [HV] (CK_RSCALE_PER_HEAD).
+ *   Slot strides are in elements of each tensor.
+ * out [B, 1, HV, V] contiguous, dtype out_dtype.
+ * ssm_state_indices [B] int32 (stride in elements): slot <= 0 is the NULL
+ *   block (out gets zeros, state untouched); slot >= num_slots is out of range
+ *   (out gets NaN, state untouched).
+ * state_bits: the state code range is +-(2^(state_bits-1) - 1), bits in 2..8.
+ * Requirements: K in {16, 32, 64, 128, 256}; HV % H == 0; 16-byte aligned
+ *   state rows (8-byte for int4 residual rows).
+ */
+int ck_gdn_packed_decode(const void* mixed_qkv, int qkv_dtype, int64_t stride_qkv_tok,
+                         const void* a, int a_dtype, int64_t stride_a_tok,
+                         const void* b, int b_dtype, int64_t stride_b_tok,
+                         const void* A_log, int A_log_dtype,
+                         const void* dt_bias, int dt_bias_dtype,
+                         float scale,
+                         int8_t* state_codes, int64_t stride_state_slot,
+                         float* state_scale, int64_t stride_sscale_slot,
+                         int8_t* resid_codes, int64_t stride_resid_slot,
+                         float* resid_scale, int64_t stride_rscale_slot,
+                         void* out, int out_dtype,
+                         const int32_t* ssm_state_indices, int64_t stride_indices,
+                         int64_t num_slots,
+                         int B, int H, int HV, int K, int V,
+                         int use_qk_l2norm, int resid_fmt, int rscale_mode,
+                         int state_bits, int quant_mode,
+                         void* stream);
+
+/*
+ * Same step with an unquantized state pool (fp32 or bf16), the layout and
+ * semantics of the upstream packed decode that the quantized op replaces:
+ * state per slot contiguous [HV, V, K] of state_dtype, updated in place
+ * (bf16 stores round to nearest even).
+ */
+int ck_gdn_packed_decode_float_state(const void* mixed_qkv, int qkv_dtype, int64_t stride_qkv_tok,
+                                     const void* a, int a_dtype, int64_t stride_a_tok,
+                                     const void* b, int b_dtype, int64_t stride_b_tok,
+                                     const void* A_log, int A_log_dtype,
+                                     const void* dt_bias, int dt_bias_dtype,
+                                     float scale,
+                                     void* state, int state_dtype, int64_t stride_state_slot,
+                                     void* out, int out_dtype,
+                                     const int32_t* ssm_state_indices, int64_t stride_indices,
+                                     int64_t num_slots,
+                                     int B, int H, int HV, int K, int V,
+                                     int use_qk_l2norm, void* stream);
+
+/*
+ * One out-of-place step in the statequant layout: state [B, HV, K, V] int8
+ * (V contiguous) with one scale per V-column (amax over K), residual e of
+ * res_fmt (fp32 / fp16 / fp8 e5m2 / int8 with a per-V-column e_scale).
+ * q, k [B, HV, K]; v [B, HV, V]; alpha, beta [B, HV]; all fp32, contiguous.
+ * qmax = 2^(bits-1) - 1 is used for the state and, for CK_RES_INT8, for the
+ * residual, as the reference's GPU kernels do (cuda/gdn_state_kernel.cu:210,233).
+ * e_scale_in / e_scale_out are read / written only for CK_RES_INT8.
+ * In-place use (h_out == h_in, e_out == e_in, ...) is allowed.
+ * Requirements: K in {16, 32, 64, 128}.
+ */
+int ck_gdn_quant_step(const int8_t* h_in, const float* scale_in, const void* e_in,
+                      const float* e_scale_in,
+                      const float* q, const float* k, const float* v,
+                      const float* alpha, const float* beta,
+                      float* o, int8_t* h_out, float* scale_out, void* e_out, float* e_scale_out,
+                      int B, int HV, int K, int V, float qmax, int res_fmt, int quant_mode,
+                      void* stream);
+
+/* FP32 baseline step in the statequant layout (no quantization). */
+int ck_gdn_fp32_step(const float* h_in, const float* q, const float* k, const float* v,
+                     const float* alpha, const float* beta, float* o, float* h_out,
+                     int B, int HV, int K, int V, void* stream);
+
+/*
+ * Quantize rows of length K (contiguous, row stride `stride_row` elements) to
+ * int8 codes with one scale per row: scale = max(amax, 1e-12) / qmax,
+ * code = rne(x / scale) clamped to +-qmax (init_quantized_state semantics).
+ * codes are written contiguous [rows, K], scales [rows].
+ */
+int ck_quantize_rows(const void* x, int x_dtype, int64_t stride_row, int64_t rows, int K,
+                     float qmax, int8_t* codes, float* scale, void* stream);
+
+/*
+ * Quantize M contiguous [K, V] matrices per V-column (amax over K), same
+ * arithmetic as ck_quantize_rows: codes [M, K, V], scale [M, V].
+ */
+int ck_quantize_cols(const float* x, int64_t M, int K, int V, float qmax,
+                     int8_t* codes, float* scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CARRYKERNEL_GDN_H_ */

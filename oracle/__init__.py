@@ -1,0 +1,209 @@
+"""CPU oracle for the fused GDN decode step with EF state quantization.
+
+TEST INFRASTRUCTURE ONLY. Imported by ``tests/``, ``__graft_entry__.smoke()``
+and the CPU-baseline leg of ``bench.py``, always as the checker. The product
+package (``carrykernel_amd``) never imports it.
+
+The arithmetic lives in ``gdn_oracle.c`` (built by ``oracle/Makefile`` into
+``oracle/lib/libgdn_oracle.so``); this module is its numpy front end plus a few
+pure-numpy restatements used to pin the C code (nibble packing, the
+float64 GDN recurrence, bf16 rounding). Each function cites the reference
+file:line it restates.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+import threading
+
+import numpy as np
+
+ORACLE_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(ORACLE_DIR, "lib", "libgdn_oracle.so")
+
+MODE_FAST = 0
+MODE_EXACT = 1
+
+RESID_INT8 = 0
+RESID_INT4 = 1
+
+_lock = threading.Lock()
+_lib = None
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_i8p = np.ctypeslib.ndpointer(dtype=np.int8, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_flt = ctypes.c_float
+
+
+def build() -> str:
+    """Compile the C oracle with its Makefile (always rebuilds)."""
+    subprocess.run(["make", "-B", "-s", "-C", ORACLE_DIR], check=True,
+                   capture_output=True, text=True)
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                build()
+            L = ctypes.CDLL(LIB_PATH)
+            L.orc_expf_n.argtypes = [_f32p, _f32p, _i64]
+            L.orc_logf_n.argtypes = [_f32p, _f32p, _i64]
+            L.orc_gates_n.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _i64]
+            L.orc_packed_decode.restype = _int
+            L.orc_packed_decode.argtypes = [
+                _f32p, _i64, _f32p, _i64, _f32p, _i64, _f32p, _f32p, _flt,
+                _i8p, _i64, _f32p, _i64, _i8p, _i64, _f32p, _i64,
+                _f32p, _i32p, _i64,
+                _int, _int, _int, _int, _int,
+                _int, _int, _int, _int, _int, _int]
+            L.orc_quantize_rows.argtypes = [_f32p, _i64, _int, _flt, _i8p, _f32p]
+            L.orc_quantize_cols.argtypes = [_f32p, _i64, _int, _int, _flt, _i8p, _f32p]
+            _lib = L
+    return _lib
+
+
+def _f32(x) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+
+
+# ---------------------------------------------------------------------------
+# Gate math
+# ---------------------------------------------------------------------------
+
+def expf(x) -> np.ndarray:
+    x = _f32(x).ravel()
+    y = np.empty_like(x)
+    lib().orc_expf_n(x, y, x.size)
+    return y
+
+
+def logf(x) -> np.ndarray:
+    x = _f32(x).ravel()
+    y = np.empty_like(x)
+    lib().orc_logf_n(x, y, x.size)
+    return y
+
+
+def gates(a, b, A_log, dt_bias):
+    """alpha, beta per quantized_packed_decode.py:179-182 (arrays broadcast)."""
+    a, b, A_log, dt_bias = np.broadcast_arrays(_f32(a), _f32(b), _f32(A_log), _f32(dt_bias))
+    shape = a.shape
+    a, b, A_log, dt_bias = (_f32(x).ravel() for x in (a, b, A_log, dt_bias))
+    alpha = np.empty_like(a)
+    beta = np.empty_like(a)
+    lib().orc_gates_n(a, b, A_log, dt_bias, alpha, beta, a.size)
+    return alpha.reshape(shape), beta.reshape(shape)
+
+
+# ---------------------------------------------------------------------------
+# vLLM-layout step
+# ---------------------------------------------------------------------------
+
+def packed_decode(mixed_qkv, a, b, A_log, dt_bias, scale,
+                  state_codes, state_scale, resid_codes, resid_scale,
+                  indices, H, *, use_qk_l2norm=False, resid_fmt=RESID_INT8,
+                  per_head=False, state_bits=8, mode=MODE_FAST, nthreads=0):
+    """One step of quantized_packed_decode.py:116-239 on host arrays.
+
+    The pool arrays (``state_codes [S,HV,V,K]`` int8, ``state_scale [S,HV,V]``,
+    ``resid_codes [S,HV,V,K or K/2]`` int8, ``resid_scale [S,HV,V]`` or
+    ``[S,HV]`` when ``per_head``) are updated in place and must be
+    C-contiguous numpy arrays. Returns ``out [B, HV, V]`` fp32.
+    """
+    mixed = _f32(mixed_qkv)
+    a = _f32(a)
+    b = _f32(b)
+    A_log = _f32(A_log)
+    dt_bias = _f32(dt_bias)
+    idx = np.ascontiguousarray(np.asarray(indices, dtype=np.int32))
+    for arr, dt in ((state_codes, np.int8), (resid_codes, np.int8),
+                    (state_scale, np.float32), (resid_scale, np.float32)):
+        if arr.dtype != dt or not arr.flags.c_contiguous:
+            raise ValueError("pool arrays must be C-contiguous with the right dtype")
+    S, HV, V, K = state_codes.shape
+    B = mixed.shape[0]
+    out = np.empty((B, HV, V), dtype=np.float32)
+    rc = lib().orc_packed_decode(
+        mixed, mixed.shape[1], a, a.shape[1], b, b.shape[1], A_log, dt_bias, float(scale),
+        state_codes, state_codes[0].size, state_scale, state_scale[0].size,
+        resid_codes, resid_codes[0].size, resid_scale, resid_scale[0].size,
+        out, idx, S, B, H, HV, K, V,
+        int(bool(use_qk_l2norm)), int(resid_fmt), int(bool(per_head)), int(state_bits),
+        int(mode), int(nthreads))
+    if rc != 0:
+        raise ValueError("oracle: unsupported shape")
+    return out
+
+
+def quantize_rows(x, qmax=127.0):
+    """init_quantized_state seeding (quantized_packed_decode.py:347-351), last dim."""
+    x = _f32(x)
+    K = x.shape[-1]
+    rows = x.size // K
+    codes = np.empty(x.shape, dtype=np.int8)
+    scale = np.empty(x.shape[:-1], dtype=np.float32)
+    lib().orc_quantize_rows(x, rows, K, float(qmax), codes, scale)
+    return codes, scale
+
+
+def quantize_cols(x, qmax=127.0):
+    """per_v_channel_quantize (statequant/kernel.py:99-113): [..., K, V], amax over K."""
+    x = _f32(x)
+    K, V = x.shape[-2:]
+    M = x.size // (K * V)
+    codes = np.empty(x.shape, dtype=np.int8)
+    scale = np.empty(x.shape[:-2] + (V,), dtype=np.float32)
+    lib().orc_quantize_cols(x, M, K, V, float(qmax), codes, scale)
+    return codes, scale
+
+
+# ---------------------------------------------------------------------------
+# numpy restatements used to pin the C code
+# ---------------------------------------------------------------------------
+
+def pack_int4(codes: np.ndarray) -> np.ndarray:
+    """quantized_packed_decode.py:226-230: byte = (c_even & 0xF) | (c_odd & 0xF) << 4."""
+    c = np.asarray(codes).astype(np.int32)
+    lo = c[..., 0::2] & 0xF
+    hi = (c[..., 1::2] & 0xF) << 4
+    return (lo | hi).astype(np.uint8).view(np.int8)
+
+
+def unpack_int4(packed: np.ndarray) -> np.ndarray:
+    """quantized_packed_decode.py:196-199: even K low nibble, odd K high, >7 -> -16."""
+    p = np.asarray(packed).astype(np.int32) & 0xFF
+    lo = p & 0xF
+    hi = (p >> 4) & 0xF
+    lo = np.where(lo > 7, lo - 16, lo)
+    hi = np.where(hi > 7, hi - 16, hi)
+    out = np.empty(p.shape[:-1] + (p.shape[-1] * 2,), dtype=np.int32)
+    out[..., 0::2] = lo
+    out[..., 1::2] = hi
+    return out
+
+
+def bf16_round(x: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 (round to nearest even) -> fp32."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16 << 16
+    return (u & 0xFFFFFFFF).astype(np.uint32).view(np.float32)
+
+
+def gdn_step_f64(h, q, k, v, alpha, beta):
+    """statequant/reference.py:20-34 in float64 on a [.., K, V] state."""
+    h = np.asarray(h, np.float64) * np.asarray(alpha, np.float64)[..., None, None]
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    read = np.einsum("...kv,...k->...v", h, k)
+    dv = np.asarray(beta, np.float64)[..., None] * (np.asarray(v, np.float64) - read)
+    h = h + k[..., :, None] * dv[..., None, :]
+    o = np.einsum("...kv,...k->...v", h, q)
+    return h, o

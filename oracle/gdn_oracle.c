@@ -1,0 +1,368 @@
+/*
+ * CPU oracle for the fused GDN decode step with error-feedback state
+ * quantization. TEST INFRASTRUCTURE ONLY: it is loaded by tests/, by
+ * __graft_entry__.smoke() and by bench.py's CPU-baseline leg, as the checker;
+ * the product never calls it.
+ *
+ * It restates the reference algorithm in plain C, one (request, value-head)
+ * at a time:
+ *   vllm_integration/quantized_packed_decode.py:116-239   (vLLM layout step)
+ *   statequant/kernel.py:149-178 and :260-341             (statequant layout step)
+ *   statequant/kernel.py:116-123, cuda/gdn_state_kernel.cu:251-297 (fp32 step)
+ *   statequant/reference.py:20-34                         (GDN recurrence)
+ *   statequant/quant.py:37-42, :65-80                     (per-axis quantizer, EF)
+ *   vllm_integration/quantized_packed_decode.py:347-351   (init quantize)
+ *
+ * The reference leaves the fp32 evaluation order of its K-reductions to
+ * torch.einsum / Triton and the quantizer's division to the backend. This
+ * oracle fixes both, so that a GPU implementation following the same order is
+ * checked bit for bit:
+ *  - A K-reduction (dot product) is split into chunks of 16 consecutive K;
+ *    each chunk is x0*y0 followed by fmaf(xj, yj, acc) for j = 1..15, and the
+ *    K/16 chunk sums are combined as a balanced pairwise tree
+ *    ((c0+c1)+(c2+c3))+((c4+c5)+(c6+c7)) ....
+ *  - FAST quantizer mode: code = rne(t * RN(1/s)) of the exact product, the
+ *    residual is fmaf(-code, s, t), dequantize-decay is code * RN(s*alpha),
+ *    rank-1 update and residual add are fmaf.
+ *  - EXACT quantizer mode: code = rne(RN(t / s)) with an IEEE division, the
+ *    residual is RN(t - RN(code*s)), dequantize-decay is RN(RN(code*s)*alpha),
+ *    rank-1 update and residual add are RN(a + RN(x*y)): the op-by-op rounding
+ *    of statequant/kernel.py:165-177.
+ * Clamping to +-qmax is applied (as the reference does); it never binds.
+ * Build: see oracle/Makefile (-ffp-contract=off keeps every a*b+c unfused).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define ORC_EPS 1e-12f
+
+/* ------------------------------------------------------------------------- */
+/* Gate transcendentals: Cody-Waite exp with a degree-8 Taylor polynomial and  */
+/* an atanh-series log, the method the kernels use (same fp32 operation        */
+/* sequence, so the same bits). Accuracy is checked against float64 by tests. */
+/* ------------------------------------------------------------------------- */
+static float orc_bits_to_float(uint32_t u) {
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+static uint32_t orc_float_to_bits(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return u;
+}
+static float orc_pow2i(int n) { return orc_bits_to_float((uint32_t)(n + 127) << 23); }
+
+float orc_expf(float x) {
+  if (x != x) return x;
+  if (x > 88.72283172607421875f) return orc_bits_to_float(0x7f800000u);
+  if (x < -103.97208404541015625f) return 0.0f;
+  const float n = rintf(x * 1.44269502162933349609375f);
+  float r = fmaf(-n, 0.693145751953125f, x);
+  r = fmaf(-n, 1.42860676533018704503775e-06f, r);
+  float p = 2.48015873015873015873e-05f;
+  p = fmaf(p, r, 1.98412698412698412698e-04f);
+  p = fmaf(p, r, 1.38888888888888888889e-03f);
+  p = fmaf(p, r, 8.33333333333333333333e-03f);
+  p = fmaf(p, r, 4.16666666666666666667e-02f);
+  p = fmaf(p, r, 1.66666666666666666667e-01f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  const int ni = (int)n;
+  const int n1 = ni / 2;
+  const int n2 = ni - n1;
+  return (p * orc_pow2i(n1)) * orc_pow2i(n2);
+}
+
+float orc_logf(float y) {
+  if (y != y || y < 0.0f) return orc_bits_to_float(0x7fc00000u);
+  if (y == 0.0f) return orc_bits_to_float(0xff800000u);
+  if (y > 3.40282346638528859812e+38f) return y;
+  int e = 0;
+  if (y < 1.17549435082228750797e-38f) {
+    y = y * 16777216.0f;
+    e = -24;
+  }
+  const uint32_t u = orc_float_to_bits(y);
+  e += (int)((u >> 23) & 0xffu) - 127;
+  float m = orc_bits_to_float((u & 0x007fffffu) | 0x3f800000u);
+  if (m > 1.41421353816986083984f) {
+    m = m * 0.5f;
+    e += 1;
+  }
+  const float s = (m - 1.0f) / (m + 1.0f);
+  const float s2 = s * s;
+  float p = 7.69230769230769230769e-02f;
+  p = fmaf(p, s2, 9.09090909090909090909e-02f);
+  p = fmaf(p, s2, 1.11111111111111111111e-01f);
+  p = fmaf(p, s2, 1.42857142857142857143e-01f);
+  p = fmaf(p, s2, 2.0e-01f);
+  p = fmaf(p, s2, 3.33333333333333333333e-01f);
+  const float logm = fmaf(2.0f * s, s2 * p, 2.0f * s);
+  const float fe = (float)e;
+  return fmaf(fe, 0.693145751953125f, fmaf(fe, 1.42860676533018704503775e-06f, logm));
+}
+
+/* quantized_packed_decode.py:179-182 */
+void orc_gates(float a, float b, float A_log, float dt_bias, float* alpha, float* beta) {
+  const float x = a + dt_bias;
+  const float sp = (x <= 20.0f) ? orc_logf(1.0f + orc_expf(x)) : x;
+  const float g = -orc_expf(A_log) * sp;
+  *alpha = orc_expf(g);
+  *beta = 1.0f / (1.0f + orc_expf(-b));
+}
+
+/* Vectorised entry points for tests (n values). */
+void orc_expf_n(const float* x, float* y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) y[i] = orc_expf(x[i]);
+}
+void orc_logf_n(const float* x, float* y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) y[i] = orc_logf(x[i]);
+}
+void orc_gates_n(const float* a, const float* b, const float* A_log, const float* dt_bias, float* alpha,
+                 float* beta, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) orc_gates(a[i], b[i], A_log[i], dt_bias[i], &alpha[i], &beta[i]);
+}
+
+/* ------------------------------------------------------------------------- */
+/* Reductions in the fixed order described at the top.                       */
+/* ------------------------------------------------------------------------- */
+static float tree_sum(float* c, int n) {
+  /* balanced pairwise tree over n = 1, 2, 4, 8, 16 chunk sums (in place) */
+  for (int w = 1; w < n; w *= 2)
+    for (int i = 0; i + w < n; i += 2 * w) c[i] = c[i] + c[i + w];
+  return c[0];
+}
+
+/* sum_k x[k*sx] * y[k*sy] over K (K a multiple of 16, K/16 a power of 2). */
+static float dot_k(const float* x, int64_t sx, const float* y, int64_t sy, int K) {
+  float chunk[16];
+  const int nc = K / 16;
+  for (int cidx = 0; cidx < nc; ++cidx) {
+    const float* xc = x + (int64_t)cidx * 16 * sx;
+    const float* yc = y + (int64_t)cidx * 16 * sy;
+    float acc = xc[0] * yc[0];
+    for (int j = 1; j < 16; ++j) acc = fmaf(xc[(int64_t)j * sx], yc[(int64_t)j * sy], acc);
+    chunk[cidx] = acc;
+  }
+  return tree_sum(chunk, nc);
+}
+
+/* ------------------------------------------------------------------------- */
+/* Quantizer primitives.                                                       */
+/* ------------------------------------------------------------------------- */
+#define MODE_FAST 0
+#define MODE_EXACT 1
+
+static const float kMagic = 12582912.0f;
+
+static float clampq(float c, float qmax) { return fminf(fmaxf(c, -qmax), qmax); }
+
+/* rounded code (as float) of t at scale s, inv = RN(1/s) */
+static float quant_code(float t, float s, float inv, float qmax, int mode) {
+  float c;
+  if (mode == MODE_FAST) {
+    c = fmaf(t, inv, kMagic) - kMagic; /* rne of the exact product */
+  } else {
+    c = rintf(t / s); /* rne of the IEEE quotient */
+  }
+  return clampq(c, qmax);
+}
+
+static float resid_of(float t, float c, float s, int mode) {
+  return mode == MODE_FAST ? fmaf(-c, s, t) : t - c * s;
+}
+
+static float madd(float x, float y, float a, int mode) { return mode == MODE_FAST ? fmaf(x, y, a) : a + x * y; }
+
+/* two's-complement nibble of element j of a packed int4 row (qpd:196-199) */
+static int unpack_i4(const int8_t* row, int j) {
+  const int byte = row[j >> 1] & 0xff;
+  int nib = (j & 1) ? (byte >> 4) & 0xf : byte & 0xf;
+  return nib > 7 ? nib - 16 : nib;
+}
+
+/* qpd:226-230: byte = (c_even & 0xF) | (c_odd & 0xF) << 4 */
+static void pack_i4_row(int8_t* row, const int* codes, int K) {
+  for (int j = 0; j < K; j += 2) {
+    const int byte = (codes[j] & 0xf) | ((codes[j + 1] & 0xf) << 4);
+    row[j >> 1] = (int8_t)(uint8_t)byte;
+  }
+}
+
+/* ------------------------------------------------------------------------- */
+/* vLLM-layout fused decode step ([slots, HV, V, K], in place).                */
+/* ------------------------------------------------------------------------- */
+int orc_packed_decode(const float* mixed, int64_t stride_mixed,
+                      const float* a, int64_t stride_a, const float* b, int64_t stride_b,
+                      const float* A_log, const float* dt_bias, float scale,
+                      int8_t* state, int64_t stride_state, float* sscale, int64_t stride_sscale,
+                      int8_t* resid, int64_t stride_resid, float* rscale, int64_t stride_rscale,
+                      float* out, const int32_t* idx, int64_t num_slots,
+                      int B, int H, int HV, int K, int V,
+                      int l2norm, int resid_fmt, int per_head, int state_bits, int mode, int nthreads) {
+  if (K % 16 != 0 || K > 256 || (K / 16 & (K / 16 - 1)) != 0 || HV % H != 0) return 1;
+  const float qmax = (float)((1 << (state_bits - 1)) - 1);
+  const float qmax_e = resid_fmt == 1 ? 7.0f : 127.0f;
+  const int RK = resid_fmt == 1 ? K / 2 : K;
+  const int64_t nwork = (int64_t)B * HV;
+  (void)nthreads;
+#ifdef _OPENMP
+  if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel
+#endif
+  {
+    float* q = (float*)malloc(sizeof(float) * K);
+    float* k = (float*)malloc(sizeof(float) * K);
+    float* h = (float*)malloc(sizeof(float) * K);
+    float* ebuf = (float*)malloc(sizeof(float) * (size_t)V * K);
+    int* codes = (int*)malloc(sizeof(int) * K);
+#ifdef _OPENMP
+#pragma omp for schedule(static)
+#endif
+    for (int64_t w = 0; w < nwork; ++w) {
+      const int n = (int)(w / HV);
+      const int hv = (int)(w % HV);
+      const int64_t slot = idx[n];
+      float* o = out + ((int64_t)n * HV + hv) * V;
+      if (slot <= 0 || slot >= num_slots) {
+        const float fill = slot <= 0 ? 0.0f : NAN;
+        for (int r = 0; r < V; ++r) o[r] = fill;
+        continue;
+      }
+      const int hq = hv / (HV / H);
+      const float* m = mixed + (int64_t)n * stride_mixed;
+      for (int j = 0; j < K; ++j) {
+        q[j] = m[(int64_t)hq * K + j];
+        k[j] = m[(int64_t)H * K + (int64_t)hq * K + j];
+      }
+      if (l2norm) { /* qpd:169-171 */
+        const float dq = sqrtf(dot_k(q, 1, q, 1, K) + 1e-6f);
+        const float dk = sqrtf(dot_k(k, 1, k, 1, K) + 1e-6f);
+        for (int j = 0; j < K; ++j) {
+          q[j] = q[j] / dq;
+          k[j] = k[j] / dk;
+        }
+      }
+      for (int j = 0; j < K; ++j) q[j] = q[j] * scale; /* qpd:172 */
+      float alpha, beta;
+      orc_gates(a[(int64_t)n * stride_a + hv], b[(int64_t)n * stride_b + hv], A_log[hv], dt_bias[hv], &alpha, &beta);
+
+      int8_t* st = state + slot * stride_state + (int64_t)hv * V * K;
+      float* ss = sscale + slot * stride_sscale + (int64_t)hv * V;
+      int8_t* er = resid + slot * stride_resid + (int64_t)hv * V * RK;
+      float* rs = per_head ? rscale + slot * stride_rscale + hv : rscale + slot * stride_rscale + (int64_t)hv * V;
+      const float* vv = m + 2 * (int64_t)H * K + (int64_t)hv * V;
+      const float rs_head = per_head ? rs[0] : 0.0f;
+      float ea_head = 0.0f;
+
+      for (int r = 0; r < V; ++r) {
+        int8_t* crow = st + (int64_t)r * K;
+        int8_t* erow = er + (int64_t)r * RK;
+        /* dequantize + decay (qpd:158, :185) */
+        if (mode == MODE_FAST) {
+          const float sa = ss[r] * alpha;
+          for (int j = 0; j < K; ++j) h[j] = (float)crow[j] * sa;
+        } else {
+          for (int j = 0; j < K; ++j) h[j] = ((float)crow[j] * ss[r]) * alpha;
+        }
+        /* delta rule (qpd:186-190) */
+        const float rd = dot_k(h, 1, k, 1, K);
+        const float dv = beta * (vv[r] - rd);
+        for (int j = 0; j < K; ++j) h[j] = madd(k[j], dv, h[j], mode);
+        o[r] = dot_k(h, 1, q, 1, K);
+        /* residual add (qpd:195-203) */
+        const float es_in = per_head ? rs_head : rs[r];
+        for (int j = 0; j < K; ++j) {
+          const int ec = resid_fmt == 1 ? unpack_i4(erow, j) : (int)erow[j];
+          h[j] = madd((float)ec, es_in, h[j], mode);
+        }
+        /* requantize (qpd:205-209) */
+        float am = 0.0f;
+        for (int j = 0; j < K; ++j) am = fmaxf(am, fabsf(h[j]));
+        const float s_new = fmaxf(am / qmax, ORC_EPS);
+        const float inv = 1.0f / s_new;
+        float* e = ebuf + (int64_t)r * K;
+        for (int j = 0; j < K; ++j) {
+          const float c = quant_code(h[j], s_new, inv, qmax, mode);
+          crow[j] = (int8_t)c;
+          e[j] = resid_of(h[j], c, s_new, mode);
+        }
+        ss[r] = s_new;
+        if (per_head) {
+          for (int j = 0; j < K; ++j) ea_head = fmaxf(ea_head, fabsf(e[j]));
+        } else { /* residual quantize, per V-row scale (qpd:211-215) */
+          float ea = 0.0f;
+          for (int j = 0; j < K; ++j) ea = fmaxf(ea, fabsf(e[j]));
+          const float es = fmaxf(ea / qmax_e, ORC_EPS);
+          const float inv_e = 1.0f / es;
+          for (int j = 0; j < K; ++j) codes[j] = (int)quant_code(e[j], es, inv_e, qmax_e, mode);
+          if (resid_fmt == 1) {
+            pack_i4_row(erow, codes, K);
+          } else {
+            for (int j = 0; j < K; ++j) erow[j] = (int8_t)codes[j];
+          }
+          rs[r] = es;
+        }
+      }
+      if (per_head) { /* one residual scale per (slot, head) */
+        const float es = fmaxf(ea_head / qmax_e, ORC_EPS);
+        const float inv_e = 1.0f / es;
+        for (int r = 0; r < V; ++r) {
+          const float* e = ebuf + (int64_t)r * K;
+          int8_t* erow = er + (int64_t)r * RK;
+          for (int j = 0; j < K; ++j) codes[j] = (int)quant_code(e[j], es, inv_e, qmax_e, mode);
+          if (resid_fmt == 1) {
+            pack_i4_row(erow, codes, K);
+          } else {
+            for (int j = 0; j < K; ++j) erow[j] = (int8_t)codes[j];
+          }
+        }
+        rs[0] = es;
+      }
+    }
+    free(q);
+    free(k);
+    free(h);
+    free(ebuf);
+    free(codes);
+  }
+  return 0;
+}
+
+/* ------------------------------------------------------------------------- */
+/* init_quantized_state seeding (qpd:347-351): per row of K,                  */
+/* scale = max(amax, eps) / qmax, code = clamp(rne(x / scale)).               */
+/* ------------------------------------------------------------------------- */
+void orc_quantize_rows(const float* x, int64_t rows, int K, float qmax, int8_t* codes, float* scale) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* xr = x + r * K;
+    float am = 0.0f;
+    for (int j = 0; j < K; ++j) am = fmaxf(am, fabsf(xr[j]));
+    const float s = fmaxf(am, ORC_EPS) / qmax;
+    for (int j = 0; j < K; ++j) codes[r * K + j] = (int8_t)clampq(rintf(xr[j] / s), qmax);
+    scale[r] = s;
+  }
+}
+
+/* per_v_channel_quantize (statequant/kernel.py:99-113): [M, K, V], amax over K */
+void orc_quantize_cols(const float* x, int64_t M, int K, int V, float qmax, int8_t* codes, float* scale) {
+  for (int64_t mi = 0; mi < M; ++mi) {
+    const float* xm = x + mi * K * V;
+    for (int c = 0; c < V; ++c) {
+      float am = 0.0f;
+      for (int j = 0; j < K; ++j) am = fmaxf(am, fabsf(xm[(int64_t)j * V + c]));
+      const float s = fmaxf(am, ORC_EPS) / qmax;
+      for (int j = 0; j < K; ++j)
+        codes[mi * K * V + (int64_t)j * V + c] = (int8_t)clampq(rintf(xm[(int64_t)j * V + c] / s), qmax);
+      scale[mi * V + c] = s;
+    }
+  }
+}
