@@ -215,6 +215,24 @@ def run_config(device, B, resid_fmt, per_head, steps, warmup, groups, quant_mode
     return ms, host_ms
 
 
+def copy_peak(device, mib, reps):
+    """Device-to-device copy of `mib` MiB (read + write), reps times."""
+    n = mib * (1 << 20) // 4
+    src = torch.randn(n, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    timer = Timer(device)
+    timer.start()
+    for _ in range(reps):
+        dst.copy_(src)
+    ms = timer.stop_ms() / reps
+    moved = 2 * n * 4
+    return {"copy_mib": mib, "bytes_per_copy": moved, "us_per_copy": round(ms * 1e3, 3),
+            "GBps": round(moved / (ms * 1e-3) / 1e9, 1)}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -228,6 +246,9 @@ def main():
     ap.add_argument("--sweep", action="store_true", help="also time B in {1, 8, 64, 256} and variants")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="instead: time a plain device copy of this many MiB (HBM copy peak, and the "
+                         "byte-count calibration for the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -238,6 +259,9 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
     device = torch.device("cuda", 0)
+    if args.copy_mib:
+        print(json.dumps(copy_peak(device, args.copy_mib, args.steps)), flush=True)
+        return
     resid_fmt = qpd.RESID_INT4 if args.resid == "int4" else qpd.RESID_INT8
     per_head = args.rscale == "head"
     B = args.batch

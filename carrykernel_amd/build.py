@@ -13,6 +13,7 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PKG_DIR)
@@ -21,6 +22,7 @@ INCLUDE_DIR = os.path.join(REPO_DIR, "include")
 LIB_DIR = os.path.join(PKG_DIR, "lib")
 LIB_NAME = "libcarrykernel_gdn.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
+OBJ_DIR = os.path.join(LIB_DIR, "_obj")
 
 ARCH = "gfx950"
 
@@ -34,7 +36,6 @@ HIPCC_FLAGS = [
     "-mcode-object-version=5",
     "-ffp-contract=off",
     "-fPIC",
-    "-shared",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",
     "-Wno-unused-function",
@@ -52,22 +53,37 @@ def sources() -> list[str]:
     return sorted(os.path.join(CSRC_DIR, f) for f in os.listdir(CSRC_DIR) if f.endswith(".hip"))
 
 
-def build(verbose: bool = False, extra_flags: list[str] | None = None) -> str:
-    """Compile the library; returns its path. Always recompiles."""
-    os.makedirs(LIB_DIR, exist_ok=True)
-    tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc_path(), *HIPCC_FLAGS, *(extra_flags or []),
-           f"-I{INCLUDE_DIR}", f"-I{CSRC_DIR}", *sources(), "-o", tmp]
-    if verbose:
-        print(" ".join(cmd), flush=True)
+def _run(cmd: list[str]) -> str:
     res = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass warns that it does not know the packed-fp32 feature.
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
     if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
-    if verbose and err.strip():
-        print(err, file=sys.stderr)
+        raise RuntimeError(f"hipcc failed ({res.returncode}): {' '.join(cmd)}\n{err}")
+    return err
+
+
+def build(verbose: bool = False, extra_flags: list[str] | None = None, jobs: int | None = None) -> str:
+    """Compile every source (in parallel) and link the library; returns its
+    path. Always recompiles."""
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    hipcc = hipcc_path()
+    flags = [*HIPCC_FLAGS, *(extra_flags or []), f"-I{INCLUDE_DIR}", f"-I{CSRC_DIR}"]
+    srcs = sources()
+    objs = [os.path.join(OBJ_DIR, os.path.basename(f)[:-4] + ".o") for f in srcs]
+    cmds = [[hipcc, *flags, "-c", src, "-o", obj] for src, obj in zip(srcs, objs)]
+    jobs = jobs or max(1, min(16, len(os.sched_getaffinity(0))))
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        for cmd, err in zip(cmds, pool.map(_run, cmds)):
+            if verbose:
+                print(" ".join(cmd), flush=True)
+                if err.strip():
+                    print(err, file=sys.stderr)
+    tmp = LIB_PATH + ".tmp"
+    link = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
+    if verbose:
+        print(" ".join(link), flush=True)
+    _run(link)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

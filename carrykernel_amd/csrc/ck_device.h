@@ -36,6 +36,49 @@ __device__ __forceinline__ float load_act(const void* p, int64_t i, int dtype) {
   return (float)static_cast<const _Float16*>(p)[i];
 }
 
+// Raw bits of one activation of ESZ bytes (4: fp32, 2: bf16 / fp16) at a
+// uniform base plus a 32-bit byte offset. Conversion is deferred to
+// act_from_raw so that issuing the load never waits for its data.
+template <int ESZ>
+__device__ __forceinline__ uint32_t load_act_raw(const char* base, uint32_t off) {
+  if constexpr (ESZ == 4) {
+    return *reinterpret_cast<const uint32_t*>(base + off);
+  } else {
+    return (uint32_t)*reinterpret_cast<const uint16_t*>(base + off);
+  }
+}
+
+__device__ __forceinline__ float act_from_raw(uint32_t raw, int dtype) {
+  if (dtype == kF32) return __uint_as_float(raw);
+  if (dtype == kBF16) return __uint_as_float(raw << 16);
+  _Float16 h;
+  const uint16_t r16 = (uint16_t)raw;
+  __builtin_memcpy(&h, &r16, 2);
+  return (float)h;
+}
+
+// Access at a uniform base plus a 32-bit byte offset (lets the compiler use
+// the scalar-base + 32-bit vector-offset addressing form).
+template <typename T>
+__device__ __forceinline__ T ld_at(const void* base, uint32_t byte_off) {
+  return *reinterpret_cast<const T*>(static_cast<const char*>(base) + byte_off);
+}
+template <typename T>
+__device__ __forceinline__ void st_at(void* base, uint32_t byte_off, T v) {
+  *reinterpret_cast<T*>(static_cast<char*>(base) + byte_off) = v;
+}
+
+// Store one activation at a uniform base plus a 32-bit element offset.
+__device__ __forceinline__ void store_act_at(void* base, uint32_t i, int dtype, float v) {
+  if (dtype == kF32) {
+    st_at<float>(base, i * 4u, v);
+  } else if (dtype == kBF16) {
+    st_at<uint16_t>(base, i * 2u, f32_to_bf16_rne(v));
+  } else {
+    st_at<_Float16>(base, i * 2u, (_Float16)v);  // round to nearest even
+  }
+}
+
 __device__ __forceinline__ void store_act(void* p, int64_t i, int dtype, float v) {
   if (dtype == kF32) {
     static_cast<float*>(p)[i] = v;
@@ -92,17 +135,28 @@ __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
+// Max over a group of N lanes of non-negative floats (absolute values). For
+// x >= 0 (and +inf) the IEEE order equals the unsigned order of the bit
+// patterns, so the cross-lane steps are v_max_u32 with a fused DPP source,
+// which avoids the NaN-quieting extra op of an IEEE fmaxf on a DPP result.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xF, 0xF, false);
+}
+
 template <int N>
 __device__ __forceinline__ float group_max(float x) {
   static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16, "group size");
-  if constexpr (N >= 2) x = fmaxf(x, dpp_f<kDppQuadXor1>(x));
-  if constexpr (N >= 4) x = fmaxf(x, dpp_f<kDppQuadXor2>(x));
-  if constexpr (N >= 8) x = fmaxf(x, dpp_f<kDppRowHalfMirror>(x));
-  if constexpr (N >= 16) x = fmaxf(x, dpp_f<kDppRowMirror>(x));
-  return x;
+  uint32_t u = __float_as_uint(x);
+  if constexpr (N >= 2) u = max(u, dpp_u<kDppQuadXor1>(u));
+  if constexpr (N >= 4) u = max(u, dpp_u<kDppQuadXor2>(u));
+  if constexpr (N >= 8) u = max(u, dpp_u<kDppRowHalfMirror>(u));
+  if constexpr (N >= 16) u = max(u, dpp_u<kDppRowMirror>(u));
+  return __uint_as_float(u);
 }
 
-// Max over a whole wavefront (64 lanes), result valid in every lane.
+// Max over a whole wavefront (64 lanes) of non-negative floats, result valid
+// in every lane.
 __device__ __forceinline__ float wave_max(float x) {
   x = group_max<16>(x);
   // combine the four rows of 16 lanes through lane reads (uniform results)
@@ -143,6 +197,79 @@ __device__ __forceinline__ float code_i8(uint32_t d, int b) {
 // Sign-extended int4 code n (0..7) of dword d, as float.
 __device__ __forceinline__ float code_i4(uint32_t d, int n) {
   return (float)(int)__builtin_amdgcn_sbfe((int)d, 4 * n, 4);
+}
+
+// v_cvt_off_f32_i4 on byte B of d: sext(low nibble of that byte) / 16, exactly.
+// One VALU op per code. (Checked on gfx950 for all 256 byte values and all
+// four byte selects.)
+template <int B>
+__device__ __forceinline__ float cvt_off_i4(uint32_t d) {
+  float r;
+  if constexpr (B == 0) {
+    asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(r) : "v"(d));
+  } else if constexpr (B == 1) {
+    asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1" : "=v"(r) : "v"(d));
+  } else if constexpr (B == 2) {
+    asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(r) : "v"(d));
+  } else {
+    asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(r) : "v"(d));
+  }
+  return r;
+}
+
+// Eight int4 codes of dword d (element j at bits 4j..4j+3), each divided by 16.
+__device__ __forceinline__ void decode_i4x8_div16(uint32_t d, float* out) {
+  const uint32_t hi = d >> 4;  // odd elements' nibbles moved to the low half of each byte
+  out[0] = cvt_off_i4<0>(d);
+  out[1] = cvt_off_i4<0>(hi);
+  out[2] = cvt_off_i4<1>(d);
+  out[3] = cvt_off_i4<1>(hi);
+  out[4] = cvt_off_i4<2>(d);
+  out[5] = cvt_off_i4<2>(hi);
+  out[6] = cvt_off_i4<3>(d);
+  out[7] = cvt_off_i4<3>(hi);
+}
+
+// ---------------------------------------------------------------------------
+// Correctly rounded scalar divisions without the generic IEEE division
+// sequence.
+// ---------------------------------------------------------------------------
+
+// RN(a / q) for an integer q in 1..127, given rq = RN(1 / q): Markstein's
+// correction of the reciprocal product. Checked exhaustively (all 2^23
+// mantissas of a at five exponents, every q in 1..127) to equal the IEEE
+// quotient.
+__device__ __forceinline__ float div_small_int(float a, float q, float rq) {
+  const float q0 = a * rq;
+  const float r = fmaf(-q0, q, a);
+  return fmaf(r, rq, q0);
+}
+
+// RN(1 / s) for a normal s whose reciprocal is normal: v_rcp_f32 followed by
+// one Newton step in fma form. Checked on gfx950 against the IEEE quotient for
+// all 2^23 mantissas at exponents spanning the fp32 range.
+__device__ __forceinline__ float recip_rn(float s) {
+  const float y = __builtin_amdgcn_rcpf(s);
+  const float e = fmaf(-s, y, 1.0f);
+  return fmaf(e, y, y);
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Streaming (non-temporal) 16- and 8-byte accesses: the state and residual are
+// touched once per step, so they should not displace reusable lines.
+__device__ __forceinline__ u32x4 ld_stream16(const int8_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ __forceinline__ u32x2 ld_stream8(const int8_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+}
+__device__ __forceinline__ void st_stream16(int8_t* p, u32x4 v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
+__device__ __forceinline__ void st_stream8(int8_t* p, u32x2 v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x2*>(p));
 }
 
 }  // namespace ck

@@ -1,0 +1,585 @@
+// Fused GDN decode step with INT8 per-V-row state and INT8 / packed-INT4
+// error-feedback residual, in vLLM's paged [slots, HV, V, K] layout (K
+// contiguous), updated in place. Counterpart of
+// vllm_integration/quantized_packed_decode.py:101-239 (device) and :242-327
+// (host launcher), written for gfx950. The templates are instantiated per K in
+// packed_decode_k*.hip; ck_gdn_packed_decode (packed_decode.hip) dispatches.
+//
+// Work items. An item is one (request, value-head, V-tile); with a per-head
+// residual scale the tile is the whole head. A workgroup of WAVES waves covers
+// a tile: a lane owns 16 consecutive K of a V-row (one 16-byte load of state
+// codes, one 8-byte (int4) or 16-byte (int8) load of residual codes), LPR =
+// K/16 lanes cover a row, one wave instruction covers 64/LPR consecutive rows
+// (a contiguous 1 KB span at K=128), and each lane keeps RPL rows. The tile
+// stays in VGPRs from load to store: state and residual are read once and
+// written once.
+//
+// Persistence and pipelining. The grid holds as many workgroups as fit on the
+// GPU at once; each loops over items (blockIdx.x, + gridDim.x, ...). While an
+// item is computed, the next item's codes, residual, scales, v and q/k are
+// loading into a second register set, so HBM streams continuously instead of
+// every resident workgroup loading, then computing, in lockstep. Prefetches
+// carry raw bits (activation conversion happens at use), so issuing them never
+// waits. q and k are staged once per item through LDS (double-buffered, one
+// barrier per item). The gates of all of a workgroup's items are evaluated
+// together, one item per lane, and read back with v_readlane.
+//
+// Arithmetic per row (FAST mode; EXACT differs where ck_quant.h says):
+//   sa = s_in * alpha;  h_j = code_j * sa
+//   rd = sum_j h_j k_j;  dv = beta * (v - rd);  h_j = fma(k_j, dv, h_j)
+//   o  = sum_j h_j q_j
+//   t_j = fma(e_code_j, e_scale_in, h_j)
+//   s = max(amax_j |t_j| / qmax, 1e-12);  code_j = rne(t_j * RN(1/s))
+//   e_j = fma(-code_j, s, t_j)
+//   es = max(amax |e| / qmax_e, 1e-12);  e_code_j = rne(e_j * RN(1/es))
+// K-sums are 16-element fma chains per lane combined by a DPP butterfly. The
+// clamps of the reference (quantized_packed_decode.py:208,215) are omitted:
+// |t_j| <= amax and s >= RN(amax/qmax) bound |t_j / s| by qmax * (1 + 2^-23)
+// < qmax + 1/2, so no rounded code exceeds qmax.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "ck_capi_common.h"
+#include "ck_device.h"
+#include "ck_quant.h"
+
+namespace ck {
+namespace pd {
+
+// Unsigned division by a runtime constant d as (x * m) >> (31 + l), exact for
+// 0 <= x < 2^31 with l = ceil(log2 d), m = ceil(2^(31+l) / d) < 2^32
+// (Granlund & Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994, Theorem 4.2 with N = 31).
+// For l >= 1, (x * m) >> (31 + l) = mulhi(x, m) >> (l - 1), a scalar
+// s_mul_hi_u32 on uniform operands; d = 1 is passed through.
+struct FastDiv {
+  uint32_t d, m, sh;  // sh = l - 1 (unused when d == 1)
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+  uint32_t l = 0;
+  while ((1ull << l) < d) ++l;
+  const uint64_t m = ((1ull << (31 + l)) + d - 1) / d;
+  return FastDiv{d, (uint32_t)m, l == 0 ? 0u : l - 1};
+}
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t x, const FastDiv& f) {
+  return f.d == 1 ? x : (__umulhi(x, f.m) >> f.sh);
+}
+
+struct PackedParams {
+  const void* mixed;
+  const void* a;
+  const void* b;
+  const void* A_log;
+  const void* dt_bias;
+  int8_t* state;
+  float* sscale;
+  int8_t* resid;
+  float* rscale;
+  void* out;
+  const int32_t* idx;
+  // strides in elements; validated on the host to fit in 32 bits
+  int32_t stride_mixed, stride_a, stride_b, stride_state, stride_sscale, stride_resid, stride_rscale, stride_idx;
+  int32_t num_slots;
+  float scale;
+  float qmax, rqmax;      // state code range and RN(1/qmax)
+  float qmax_e, rqmax_e;  // residual code range and RN(1/qmax_e)
+  int32_t dtypes;         // mixed | a << 4 | b << 8 | A_log << 12 | dt_bias << 16 | out << 20
+  int32_t H, HV, V;
+  int32_t items;          // B * HV * nvt
+  int32_t l2norm;
+  FastDiv div_nvt, div_hv;  // nvt = V-tiles per (request, head)
+
+  __device__ __forceinline__ int mixed_dtype() const { return dtypes & 15; }
+  __device__ __forceinline__ int a_dtype() const { return (dtypes >> 4) & 15; }
+  __device__ __forceinline__ int b_dtype() const { return (dtypes >> 8) & 15; }
+  __device__ __forceinline__ int A_log_dtype() const { return (dtypes >> 12) & 15; }
+  __device__ __forceinline__ int dt_bias_dtype() const { return (dtypes >> 16) & 15; }
+  __device__ __forceinline__ int out_dtype() const { return (dtypes >> 20) & 15; }
+};
+
+constexpr int kResidInt8 = CK_RESID_INT8;
+constexpr int kResidInt4 = CK_RESID_INT4;
+
+template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD>
+struct Layout {
+  static constexpr int LPR = K / 16;    // lanes per V-row
+  static constexpr int RPI = 64 / LPR;  // rows per wave instruction
+  static constexpr int ROWS_WAVE = RPI * RPL;
+  static constexpr int ROWS_WG = ROWS_WAVE * WAVES;
+  static constexpr int NT = WAVES * 64;
+  static constexpr int QKT = (2 * K + NT - 1) / NT;  // staged q/k values per thread
+  static constexpr int EW = (RESID == kResidInt4) ? 2 : 4;
+  static constexpr int RK = (RESID == kResidInt4) ? K / 2 : K;  // residual bytes per row
+};
+
+// Everything one lane needs from memory for one item.
+template <int RPL, int EW, int QKT>
+struct ItemRegs {
+  u32x4 cw[RPL];         // state codes, 16 per row
+  uint32_t ew[RPL][EW];  // residual codes
+  float s_in[RPL];       // state scale per row
+  float es_in[RPL];      // residual scale per row (per-row mode); [0] per head
+  uint32_t vv[RPL];      // v per row (raw activation bits)
+  uint32_t qk[QKT];      // this thread's share of [q | k] (raw activation bits)
+};
+
+struct ItemCoord {
+  int n, hv, vt;
+  int64_t slot;
+  bool live;  // slot in [1, num_slots)
+};
+
+// Coordinates of an item. `item` is uniform; readfirstlane keeps the results
+// in SGPRs so that the slot id is a scalar load (a vector load here would be
+// ordered behind the prefetch in the vector memory counter).
+__device__ __forceinline__ ItemCoord item_coord(const PackedParams& p, const int32_t* __restrict__ idx, int item) {
+  ItemCoord ic;
+  item = __builtin_amdgcn_readfirstlane(item);
+  const uint32_t nh = fdiv((uint32_t)item, p.div_nvt);
+  ic.vt = item - (int)(nh * p.div_nvt.d);
+  const uint32_t n = fdiv(nh, p.div_hv);
+  ic.hv = __builtin_amdgcn_readfirstlane((int)(nh - n * p.div_hv.d));
+  ic.n = __builtin_amdgcn_readfirstlane((int)n);
+  ic.vt = __builtin_amdgcn_readfirstlane(ic.vt);
+  ic.slot = (int64_t)idx[(int64_t)ic.n * p.stride_idx];
+  ic.live = ic.slot > 0 && ic.slot < p.num_slots;
+  return ic;
+}
+
+// Issue every load of one item, branch-free: the number of loads is the same
+// on every path, so the compiler's wait counts let this item's loads stay in
+// flight while the previous item is computed. A prefetch that is not needed
+// (dead item: NULL or out-of-range slot; past the last item) collapses every
+// lane onto the first bytes of slot 0 / head 0, one cache line per load, and
+// its values are never used. Rows past V re-read row V-1. Bases are uniform;
+// per-lane offsets are 32-bit.
+template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int ESZ>
+__device__ __forceinline__ void load_item(const PackedParams& p, const ItemCoord& ic, bool needed, int row0, int c,
+                                          ItemRegs<RPL, Layout<K, RPL, WAVES, RESID, PER_HEAD>::EW,
+                                                   Layout<K, RPL, WAVES, RESID, PER_HEAD>::QKT>& R) {
+  using L = Layout<K, RPL, WAVES, RESID, PER_HEAD>;
+  const bool real = needed && ic.live;
+  const uint32_t keep = real ? 0xffffffffu : 0u;  // per-lane offset mask
+  const int64_t slot = real ? ic.slot : 0;
+  const int hv = real ? ic.hv : 0;
+  const int8_t* sbase = p.state + slot * p.stride_state + (int64_t)hv * p.V * K;
+  const int8_t* ebase = p.resid + slot * p.stride_resid + (int64_t)hv * p.V * L::RK;
+  const float* scb = p.sscale + slot * p.stride_sscale + (int64_t)hv * p.V;
+  const float* rsb = p.rscale + slot * p.stride_rscale + (int64_t)hv * p.V;  // per-row mode only
+  const char* mrow = static_cast<const char*>(p.mixed) + (int64_t)ic.n * p.stride_mixed * ESZ;
+  const char* vbase = mrow + (2 * (int64_t)p.H * K + (int64_t)hv * p.V) * ESZ;
+#pragma unroll
+  for (int i = 0; i < RPL; ++i) {
+    const uint32_t r = (uint32_t)min(row0 + i * L::RPI, p.V - 1) & keep;
+    const uint32_t cc = (uint32_t)c & keep;
+    R.cw[i] = ld_stream16(sbase + (r * K + cc * 16));
+    if constexpr (RESID == kResidInt4) {
+      const u32x2 t = ld_stream8(ebase + (r * L::RK + cc * 8));
+      R.ew[i][0] = t.x;
+      R.ew[i][1] = t.y;
+    } else {
+      const u32x4 t = ld_stream16(ebase + (r * L::RK + cc * 16));
+      R.ew[i][0] = t.x;
+      R.ew[i][1] = t.y;
+      R.ew[i][2] = t.z;
+      R.ew[i][3] = t.w;
+    }
+    R.s_in[i] = ld_at<float>(scb, r * 4u);
+    if constexpr (!PER_HEAD) R.es_in[i] = ld_at<float>(rsb, r * 4u);
+    R.vv[i] = load_act_raw<ESZ>(vbase, r * ESZ);
+  }
+  if constexpr (PER_HEAD) {
+    // one scale per (slot, head), loaded by every lane (a vector load, so it
+    // is ordered with the other prefetches)
+    const float* rsh = p.rscale + slot * p.stride_rscale + hv;
+    R.es_in[0] = ld_at<float>(rsh, 0u * (uint32_t)c);
+  }
+  const char* qbase = mrow + (int64_t)(hv / (p.HV / p.H)) * K * ESZ;
+  const uint32_t koff = (uint32_t)((p.H - 1) * K);  // k of this head sits H*K after q
+#pragma unroll
+  for (int j = 0; j < L::QKT; ++j) {
+    const uint32_t e = min((uint32_t)threadIdx.x + j * L::NT, (uint32_t)(2 * K - 1));  // q then k
+    R.qk[j] = load_act_raw<ESZ>(qbase, ((e < K ? e : e + koff) * ESZ) & keep);
+  }
+}
+
+template <int RESID>
+__device__ __forceinline__ void store_resid(int8_t* dst, const uint32_t (&eb)[16]) {
+  if constexpr (RESID == kResidInt4) {
+    const uint32_t w0[8] = {eb[0], eb[1], eb[2], eb[3], eb[4], eb[5], eb[6], eb[7]};
+    const uint32_t w1[8] = {eb[8], eb[9], eb[10], eb[11], eb[12], eb[13], eb[14], eb[15]};
+    st_stream8(dst, u32x2{pack_nibbles8(w0), pack_nibbles8(w1)});
+  } else {
+    st_stream16(dst, u32x4{pack_low_bytes(eb[0], eb[1], eb[2], eb[3]), pack_low_bytes(eb[4], eb[5], eb[6], eb[7]),
+                           pack_low_bytes(eb[8], eb[9], eb[10], eb[11]),
+                           pack_low_bytes(eb[12], eb[13], eb[14], eb[15])});
+  }
+}
+
+// Compute and store one item whose registers are loaded.
+template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE>
+__device__ __forceinline__ void process_item(const PackedParams& p, const ItemCoord& ic, int row0, int c, int lane,
+                                             int wave, int parity, float alpha, float beta,
+                                             const ItemRegs<RPL, Layout<K, RPL, WAVES, RESID, PER_HEAD>::EW,
+                                                            Layout<K, RPL, WAVES, RESID, PER_HEAD>::QKT>& R,
+                                             float (*s_qk)[2 * K], float (*s_red)[WAVES]) {
+  using L = Layout<K, RPL, WAVES, RESID, PER_HEAD>;
+  constexpr int LPR = L::LPR;
+  const int odt = p.out_dtype();
+  char* obase = static_cast<char*>(p.out) + ((int64_t)ic.n * p.HV + ic.hv) * p.V * (odt == kF32 ? 4 : 2);
+
+  if (!ic.live) {
+    // NULL block (slot <= 0): zeros, no state access
+    // (quantized_packed_decode.py:132-136); out-of-range ids: NaN.
+    const float fill = (ic.slot <= 0) ? 0.0f : __uint_as_float(0x7fc00000u);
+    if (c == 0) {
+#pragma unroll
+      for (int i = 0; i < RPL; ++i) {
+        const int r = row0 + i * L::RPI;
+        if (r < p.V) store_act_at(obase, (uint32_t)r, odt, fill);
+      }
+    }
+    return;
+  }
+
+  // ---- stage q, k through LDS; L2 norm and q scale once per value ----
+  float* buf = s_qk[parity];
+  if (p.l2norm) {
+    float* raw = s_qk[2 + parity];
+#pragma unroll
+    for (int j = 0; j < L::QKT; ++j) {
+      const int e = (int)threadIdx.x + j * L::NT;
+      if (e < 2 * K) raw[e] = act_from_raw(R.qk[j], p.mixed_dtype());
+    }
+    __syncthreads();
+    float sq, sk;
+    {
+      const float4* q4 = reinterpret_cast<const float4*>(raw + c * 16);
+      const float4* k4 = reinterpret_cast<const float4*>(raw + K + c * 16);
+      float qv[16], kv[16];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 a4 = q4[j], b4 = k4[j];
+        qv[4 * j] = a4.x, qv[4 * j + 1] = a4.y, qv[4 * j + 2] = a4.z, qv[4 * j + 3] = a4.w;
+        kv[4 * j] = b4.x, kv[4 * j + 1] = b4.y, kv[4 * j + 2] = b4.z, kv[4 * j + 3] = b4.w;
+      }
+      sq = qv[0] * qv[0];
+      sk = kv[0] * kv[0];
+#pragma unroll
+      for (int j = 1; j < 16; ++j) {
+        sq = fmaf(qv[j], qv[j], sq);
+        sk = fmaf(kv[j], kv[j], sk);
+      }
+    }
+    sq = group_sum<LPR>(sq);
+    sk = group_sum<LPR>(sk);
+    const float dq = sqrtf(sq + 1e-6f);
+    const float dk = sqrtf(sk + 1e-6f);
+#pragma unroll
+    for (int j = 0; j < L::QKT; ++j) {
+      const int e = (int)threadIdx.x + j * L::NT;
+      if (e < 2 * K) buf[e] = (e < K) ? (raw[e] / dq) * p.scale : raw[e] / dk;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < L::QKT; ++j) {
+      const int e = (int)threadIdx.x + j * L::NT;
+      if (e < 2 * K) {
+        const float x = act_from_raw(R.qk[j], p.mixed_dtype());
+        buf[e] = (e < K) ? x * p.scale : x;
+      }
+    }
+  }
+  __syncthreads();
+  float qq[16], kk[16];
+  {
+    const float4* q4 = reinterpret_cast<const float4*>(buf + c * 16);
+    const float4* k4 = reinterpret_cast<const float4*>(buf + K + c * 16);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float4 a4 = q4[j], b4 = k4[j];
+      qq[4 * j] = a4.x, qq[4 * j + 1] = a4.y, qq[4 * j + 2] = a4.z, qq[4 * j + 3] = a4.w;
+      kk[4 * j] = b4.x, kk[4 * j + 1] = b4.y, kk[4 * j + 2] = b4.z, kk[4 * j + 3] = b4.w;
+    }
+  }
+
+  int8_t* sbase = p.state + ic.slot * p.stride_state + (int64_t)ic.hv * p.V * K;
+  int8_t* ebase = p.resid + ic.slot * p.stride_resid + (int64_t)ic.hv * p.V * L::RK;
+  float* scb = p.sscale + ic.slot * p.stride_sscale + (int64_t)ic.hv * p.V;
+  float* rsb = PER_HEAD ? p.rscale + ic.slot * p.stride_rscale + ic.hv
+                        : p.rscale + ic.slot * p.stride_rscale + (int64_t)ic.hv * p.V;
+  const float es_head = R.es_in[0];
+
+  float ekeep[PER_HEAD ? RPL : 1][16];
+  float eamax_local = 0.0f;
+
+#pragma unroll
+  for (int i = 0; i < RPL; ++i) {
+    const int r = row0 + i * L::RPI;
+    const bool valid = r < p.V;
+    const uint32_t cws[4] = {R.cw[i].x, R.cw[i].y, R.cw[i].z, R.cw[i].w};
+
+    // dequantize + decay
+    float h[16];
+    if constexpr (MODE == kFast) {
+      const float sa = R.s_in[i] * alpha;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) h[j] = code_i8(cws[j >> 2], j & 3) * sa;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) h[j] = (code_i8(cws[j >> 2], j & 3) * R.s_in[i]) * alpha;
+    }
+
+    // delta rule: rd = h^T k, dv = beta (v - rd), h += k dv, o = h^T q
+    float rd = h[0] * kk[0];
+#pragma unroll
+    for (int j = 1; j < 16; ++j) rd = fmaf(h[j], kk[j], rd);
+    rd = group_sum<LPR>(rd);
+    const float dv = beta * (act_from_raw(R.vv[i], p.mixed_dtype()) - rd);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) h[j] = madd<MODE>(kk[j], dv, h[j]);
+    float o = h[0] * qq[0];
+#pragma unroll
+    for (int j = 1; j < 16; ++j) o = fmaf(h[j], qq[j], o);
+    o = group_sum<LPR>(o);
+    if (c == 0 && valid) store_act_at(obase, (uint32_t)r, odt, o);
+
+    // add the carried residual: t = h + e_code * e_scale
+    const float es_in = PER_HEAD ? es_head : R.es_in[i];
+    float t[16];
+    if constexpr (RESID == kResidInt4) {
+      // codes arrive as code/16 (exact), so scale by 16*es (exact)
+      float ec[16];
+      decode_i4x8_div16(R.ew[i][0], ec);
+      decode_i4x8_div16(R.ew[i][1], ec + 8);
+      const float es16 = es_in * 16.0f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) t[j] = madd<MODE>(ec[j], es16, h[j]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) t[j] = madd<MODE>(code_i8(R.ew[i][j >> 2], j & 3), es_in, h[j]);
+    }
+
+    // requantize the state
+    float am = fabsf(t[0]);
+#pragma unroll
+    for (int j = 1; j < 16; ++j) am = fmaxf(am, fabsf(t[j]));
+    am = group_max<LPR>(am);
+    const float s_new = fmaxf(div_small_int(am, p.qmax, p.rqmax), kEps);
+    const float inv = recip_rn(s_new);
+    uint32_t yb[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const float code = quantize<MODE>(t[j], s_new, inv, yb[j]);
+      t[j] = residual<MODE>(t[j], code, s_new);
+    }
+    if (valid) {
+      st_stream16(sbase + (uint32_t)(r * K + c * 16),
+                  u32x4{pack_low_bytes(yb[0], yb[1], yb[2], yb[3]), pack_low_bytes(yb[4], yb[5], yb[6], yb[7]),
+                        pack_low_bytes(yb[8], yb[9], yb[10], yb[11]), pack_low_bytes(yb[12], yb[13], yb[14], yb[15])});
+      if (c == 0) st_at<float>(scb, (uint32_t)r * 4u, s_new);
+    }
+
+    float ea = fabsf(t[0]);
+#pragma unroll
+    for (int j = 1; j < 16; ++j) ea = fmaxf(ea, fabsf(t[j]));
+
+    if constexpr (PER_HEAD) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) ekeep[i][j] = t[j];
+      eamax_local = fmaxf(eamax_local, valid ? ea : 0.0f);  // rows past V hold re-read data
+    } else {
+      ea = group_max<LPR>(ea);
+      const float es = fmaxf(div_small_int(ea, p.qmax_e, p.rqmax_e), kEps);
+      const float inv_e = recip_rn(es);
+      uint32_t eb[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) (void)quantize<MODE>(t[j], es, inv_e, eb[j]);
+      if (valid) {
+        store_resid<RESID>(ebase + (uint32_t)(r * L::RK + c * (L::RK / LPR)), eb);
+        if (c == 0) st_at<float>(rsb, (uint32_t)r * 4u, es);
+      }
+    }
+  }
+
+  if constexpr (PER_HEAD) {
+    // one residual scale for the whole (slot, head)
+    const float wm = wave_max(eamax_local);
+    if (lane == 0) s_red[parity][wave] = wm;
+    __syncthreads();
+    float ea = s_red[parity][0];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) ea = fmaxf(ea, s_red[parity][w]);
+    const float es = fmaxf(div_small_int(ea, p.qmax_e, p.rqmax_e), kEps);
+    const float inv_e = recip_rn(es);
+#pragma unroll
+    for (int i = 0; i < RPL; ++i) {
+      const int r = row0 + i * L::RPI;
+      uint32_t eb[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) (void)quantize<MODE>(ekeep[i][j], es, inv_e, eb[j]);
+      if (r < p.V) store_resid<RESID>(ebase + (uint32_t)(r * L::RK + c * (L::RK / LPR)), eb);
+    }
+    if (threadIdx.x == 0) *rsb = es;
+  }
+}
+
+// Gates of this workgroup's items number kbase .. kbase+63 (one per lane).
+__device__ __forceinline__ void gates_for_items(const PackedParams& p, int kbase, int lane, float& alpha_v,
+                                                float& beta_v) {
+  const int item = (int)blockIdx.x + (kbase + lane) * (int)gridDim.x;
+  alpha_v = 1.0f;
+  beta_v = 0.0f;
+  if (item < p.items) {
+    const uint32_t nh = fdiv((uint32_t)item, p.div_nvt);
+    const uint32_t n = fdiv(nh, p.div_hv);
+    const int hv = (int)(nh - n * p.div_hv.d);
+    ck_gates(load_act(p.a, (int64_t)n * p.stride_a + hv, p.a_dtype()),
+             load_act(p.b, (int64_t)n * p.stride_b + hv, p.b_dtype()), load_act(p.A_log, hv, p.A_log_dtype()),
+             load_act(p.dt_bias, hv, p.dt_bias_dtype()), &alpha_v, &beta_v);
+  }
+}
+
+template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ESZ>
+__global__ __launch_bounds__(WAVES * 64) void packed_decode_kernel(const PackedParams p,
+                                                                   const int32_t* __restrict__ idx) {
+  using L = Layout<K, RPL, WAVES, RESID, PER_HEAD>;
+  __shared__ __attribute__((aligned(16))) float s_qk[4][2 * K];  // [parity] staged, [2 + parity] raw
+  __shared__ float s_red[2][WAVES];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c = lane % L::LPR;
+  const int g = lane / L::LPR;
+  const int stride = (int)gridDim.x;
+
+  int item = (int)blockIdx.x;
+  if (item >= p.items) return;  // whole workgroup
+  const int last = p.items - 1;
+
+  // LDS buffers alternate between consecutive live items (a NULL item skips
+  // the barriers, so the parity follows a count of live items): two uses of
+  // one buffer are always separated by the barrier of the live item between.
+  ItemRegs<RPL, L::EW, L::QKT> A, B;
+  ItemCoord ca = item_coord(p, idx, item), cb;
+  load_item<K, RPL, WAVES, RESID, PER_HEAD, ESZ>(p, ca, true, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, A);
+  float alpha_v, beta_v;
+  gates_for_items(p, 0, lane, alpha_v, beta_v);  // its loads overlap the first item's
+  int k = 0;     // item number within this workgroup
+  int live = 0;  // live items processed so far
+  for (;;) {
+    // ---- item k in A; prefetch item k+1 into B (past the end: re-read the last item) ----
+    int next = item + stride;
+    cb = item_coord(p, idx, min(next, last));
+    load_item<K, RPL, WAVES, RESID, PER_HEAD, ESZ>(p, cb, next < p.items, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, B);
+    {
+      const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), k & 63));
+      const float beta = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(beta_v), k & 63));
+      process_item<K, RPL, WAVES, RESID, PER_HEAD, MODE>(p, ca, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c,
+                                                          lane, wave, live & 1, alpha, beta, A, s_qk, s_red);
+      live += ca.live ? 1 : 0;
+    }
+    if (next >= p.items) break;
+    ++k;
+    if ((k & 63) == 0) gates_for_items(p, k, lane, alpha_v, beta_v);
+    item = next;
+
+    // ---- item k in B; prefetch item k+1 into A ----
+    next = item + stride;
+    ca = item_coord(p, idx, min(next, last));
+    load_item<K, RPL, WAVES, RESID, PER_HEAD, ESZ>(p, ca, next < p.items, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, A);
+    {
+      const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), k & 63));
+      const float beta = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(beta_v), k & 63));
+      process_item<K, RPL, WAVES, RESID, PER_HEAD, MODE>(p, cb, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c,
+                                                          lane, wave, live & 1, alpha, beta, B, s_qk, s_red);
+      live += cb.live ? 1 : 0;
+    }
+    if (next >= p.items) break;
+    ++k;
+    if ((k & 63) == 0) gates_for_items(p, k, lane, alpha_v, beta_v);
+    item = next;
+  }
+}
+
+// Resident workgroups per GPU for a kernel (occupancy x CUs), cached per device.
+int resident_workgroups(const void* fn, int block);
+
+template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ESZ>
+int launch_cfg(PackedParams p, int B, hipStream_t stream) {
+  using L = Layout<K, RPL, WAVES, RESID, PER_HEAD>;
+  const int nvt = PER_HEAD ? 1 : (p.V + L::ROWS_WG - 1) / L::ROWS_WG;
+  const int64_t items = (int64_t)B * p.HV * nvt;
+  if (items > 0x7fffffff) return fail(CK_EUNSUPPORTED, "%lld work items is too many", (long long)items);
+  if (items == 0) return ok();
+  p.items = (int)items;
+  p.div_nvt = make_fastdiv((uint32_t)nvt);
+  p.div_hv = make_fastdiv((uint32_t)p.HV);
+  auto fn = packed_decode_kernel<K, RPL, WAVES, RESID, PER_HEAD, MODE, ESZ>;
+  const int resident = resident_workgroups(reinterpret_cast<const void*>(fn), WAVES * 64);
+  if (resident <= 0) return fail(CK_ELAUNCH, "cannot query the device occupancy");
+  // fewest items per workgroup, then the fewest workgroups achieving it
+  const int per_wg = (p.items + resident - 1) / resident;
+  const int grid = (p.items + per_wg - 1) / per_wg;
+  hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(WAVES * 64), 0, stream, p, p.idx);
+  return check_launch("ck_gdn_packed_decode");
+}
+
+// Workgroup shape. K=128: a lane holds 4 rows, a wave 32 rows. With per-row
+// residual scales a workgroup is 4 waves (a whole 128-row head) when there are
+// enough heads to fill the GPU, else 1 wave (32-row tiles, 4x the items). A
+// per-head residual scale needs the whole head in one workgroup.
+template <int K, int RESID, bool PER_HEAD, int MODE, int ESZ>
+int launch_k(const PackedParams& p, int B, hipStream_t stream) {
+  constexpr int RPI = 64 / (K / 16);
+  if constexpr (!PER_HEAD) {
+    if ((int64_t)B * p.HV * ((p.V + RPI * 16 - 1) / (RPI * 16)) >= 512)
+      return launch_cfg<K, 4, 4, RESID, false, MODE, ESZ>(p, B, stream);
+    return launch_cfg<K, 4, 1, RESID, false, MODE, ESZ>(p, B, stream);
+  } else {
+    const int need = p.V;
+    if (need <= RPI * 4 * 1) return launch_cfg<K, 4, 1, RESID, true, MODE, ESZ>(p, B, stream);
+    if (need <= RPI * 4 * 2) return launch_cfg<K, 4, 2, RESID, true, MODE, ESZ>(p, B, stream);
+    if (need <= RPI * 4 * 4) return launch_cfg<K, 4, 4, RESID, true, MODE, ESZ>(p, B, stream);
+    if (need <= RPI * 4 * 8) return launch_cfg<K, 4, 8, RESID, true, MODE, ESZ>(p, B, stream);
+    return fail(CK_EUNSUPPORTED, "per-head residual scale supports V <= %d at K=%d, got V=%d", RPI * 32, K, p.V);
+  }
+}
+
+// Dispatch over residual format, scale granularity, mode and activation size
+// for one K (defined in packed_decode_k<K>.hip).
+template <int K>
+int launch_for_k(const PackedParams& p, int B, int resid_fmt, int per_head, int mode, int esz, hipStream_t stream);
+
+#define CK_PD_DEFINE_LAUNCH_FOR_K(KV)                                                                         \
+  template <>                                                                                                 \
+  int launch_for_k<KV>(const PackedParams& p, int B, int resid_fmt, int per_head, int mode, int esz,          \
+                       hipStream_t s) {                                                                       \
+    const bool i4 = resid_fmt == CK_RESID_INT4;                                                               \
+    if (esz == 4) {                                                                                           \
+      if (mode == kFast)                                                                                      \
+        return i4 ? (per_head ? launch_k<KV, kResidInt4, true, kFast, 4>(p, B, s)                                \
+                              : launch_k<KV, kResidInt4, false, kFast, 4>(p, B, s))                              \
+                  : (per_head ? launch_k<KV, kResidInt8, true, kFast, 4>(p, B, s)                                \
+                              : launch_k<KV, kResidInt8, false, kFast, 4>(p, B, s));                             \
+      return i4 ? (per_head ? launch_k<KV, kResidInt4, true, kExact, 4>(p, B, s)                                 \
+                            : launch_k<KV, kResidInt4, false, kExact, 4>(p, B, s))                               \
+                : (per_head ? launch_k<KV, kResidInt8, true, kExact, 4>(p, B, s)                                 \
+                            : launch_k<KV, kResidInt8, false, kExact, 4>(p, B, s));                              \
+    }                                                                                                         \
+    if (mode == kFast)                                                                                        \
+      return i4 ? (per_head ? launch_k<KV, kResidInt4, true, kFast, 2>(p, B, s)                                  \
+                            : launch_k<KV, kResidInt4, false, kFast, 2>(p, B, s))                                \
+                : (per_head ? launch_k<KV, kResidInt8, true, kFast, 2>(p, B, s)                                  \
+                            : launch_k<KV, kResidInt8, false, kFast, 2>(p, B, s));                               \
+    return i4 ? (per_head ? launch_k<KV, kResidInt4, true, kExact, 2>(p, B, s)                                   \
+                          : launch_k<KV, kResidInt4, false, kExact, 2>(p, B, s))                                 \
+              : (per_head ? launch_k<KV, kResidInt8, true, kExact, 2>(p, B, s)                                   \
+                          : launch_k<KV, kResidInt8, false, kExact, 2>(p, B, s));                                \
+  }
+
+}  // namespace pd
+}  // namespace ck
