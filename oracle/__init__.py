@@ -65,6 +65,23 @@ def lib():
                 _int, _int, _int, _int, _int,
                 _int, _int, _int, _int, _int, _int]
             L.orc_quantize_rows.argtypes = [_f32p, _i64, _int, _flt, _i8p, _f32p]
+            _vp = ctypes.c_void_p
+            L.orc_quant_step_kv.restype = _int
+            L.orc_quant_step_kv.argtypes = [_i8p, _f32p, _vp, _vp, _f32p, _f32p, _f32p, _f32p, _f32p,
+                                            _f32p, _i8p, _f32p, _vp, _vp,
+                                            _int, _int, _int, _int, _flt, _int, _int, _int]
+            L.orc_fp32_step_kv.restype = _int
+            L.orc_fp32_step_kv.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p,
+                                           _int, _int, _int, _int]
+            L.orc_packed_decode_float_state.restype = _int
+            L.orc_packed_decode_float_state.argtypes = [
+                _f32p, _i64, _f32p, _i64, _f32p, _i64, _f32p, _f32p, _flt,
+                _f32p, _i64, _int, _f32p, _i32p, _i64, _int, _int, _int, _int, _int, _int]
+            _u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+            _u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
+            L.orc_f32_to_f16_n.argtypes = [_f32p, _u16p, _i64]
+            L.orc_f32_to_e5m2_n.argtypes = [_f32p, _u8p, _i64]
+            L.orc_e5m2_to_f32_n.argtypes = [_u8p, _f32p, _i64]
             L.orc_quantize_cols.argtypes = [_f32p, _i64, _int, _int, _flt, _i8p, _f32p]
             _lib = L
     return _lib
@@ -163,6 +180,96 @@ def quantize_cols(x, qmax=127.0):
     scale = np.empty(x.shape[:-2] + (V,), dtype=np.float32)
     lib().orc_quantize_cols(x, M, K, V, float(qmax), codes, scale)
     return codes, scale
+
+
+# ---------------------------------------------------------------------------
+# statequant layout ([B, HV, K, V], V contiguous)
+# ---------------------------------------------------------------------------
+
+RES_FP32, RES_FP16, RES_FP8, RES_INT8 = 0, 1, 2, 3
+
+
+def f32_to_f16_bits(x) -> np.ndarray:
+    x = _f32(x)
+    y = np.empty(x.shape, np.uint16)
+    lib().orc_f32_to_f16_n(x.ravel(), y.ravel(), x.size)
+    return y
+
+
+def f32_to_e5m2_bits(x) -> np.ndarray:
+    x = _f32(x)
+    y = np.empty(x.shape, np.uint8)
+    lib().orc_f32_to_e5m2_n(x.ravel(), y.ravel(), x.size)
+    return y
+
+
+def e5m2_bits_to_f32(b) -> np.ndarray:
+    b = np.ascontiguousarray(np.asarray(b, np.uint8))
+    y = np.empty(b.shape, np.float32)
+    lib().orc_e5m2_to_f32_n(b.ravel(), y.ravel(), b.size)
+    return y
+
+
+def quant_step_kv(h_int8, scale, e, e_scale, q, k, v, alpha, beta, bits=8, res_fmt=RES_FP32,
+                  mode=MODE_FAST, nthreads=0):
+    """One out-of-place step of statequant/kernel.py:149-178 / :260-341.
+
+    ``e`` is the residual's storage: float32 values (RES_FP32), uint16 fp16
+    bits (RES_FP16), uint8 e5m2 bits (RES_FP8) or int8 codes (RES_INT8, with
+    ``e_scale``). Returns ``(o, h_int8_new, scale_new, e_new, e_scale_new)``
+    in the same storage conventions.
+    """
+    h_int8 = np.ascontiguousarray(h_int8, np.int8)
+    B, HV, K, V = h_int8.shape
+    store = {RES_FP32: np.float32, RES_FP16: np.uint16, RES_FP8: np.uint8, RES_INT8: np.int8}[res_fmt]
+    e = np.ascontiguousarray(e, store)
+    o = np.empty((B, HV, V), np.float32)
+    h_out = np.empty_like(h_int8)
+    s_out = np.empty((B, HV, V), np.float32)
+    e_out = np.empty_like(e)
+    es_in = _f32(e_scale) if res_fmt == RES_INT8 else None
+    es_out = np.empty((B, HV, V), np.float32) if res_fmt == RES_INT8 else None
+    rc = lib().orc_quant_step_kv(
+        h_int8, _f32(scale), e.ctypes.data, None if es_in is None else es_in.ctypes.data,
+        _f32(q), _f32(k), _f32(v), _f32(alpha), _f32(beta),
+        o, h_out, s_out, e_out.ctypes.data, None if es_out is None else es_out.ctypes.data,
+        B, HV, K, V, float(2 ** (bits - 1) - 1), int(res_fmt), int(mode), int(nthreads))
+    if rc != 0:
+        raise ValueError("oracle: unsupported shape")
+    return o, h_out, s_out, e_out, es_out
+
+
+def fp32_step_kv(h, q, k, v, alpha, beta):
+    """statequant/kernel.py:116-123 in the fixed reduction order. Returns (h, o)."""
+    h = _f32(h)
+    B, HV, K, V = h.shape
+    o = np.empty((B, HV, V), np.float32)
+    h_out = np.empty_like(h)
+    rc = lib().orc_fp32_step_kv(h, _f32(q), _f32(k), _f32(v), _f32(alpha), _f32(beta), o, h_out, B, HV, K, V)
+    if rc != 0:
+        raise ValueError("oracle: unsupported shape")
+    return h_out, o
+
+
+def packed_decode_float_state(mixed_qkv, a, b, A_log, dt_bias, scale, state, indices, H, *,
+                              bf16=False, use_qk_l2norm=False):
+    """vLLM-layout step on an unquantized state pool ``[S, HV, V, K]`` (fp32
+    values; rounded to bf16 after the update when ``bf16``), in place.
+    Returns ``out [B, HV, V]``."""
+    mixed = _f32(mixed_qkv)
+    if state.dtype != np.float32 or not state.flags.c_contiguous:
+        raise ValueError("state must be a C-contiguous float32 array")
+    S, HV, V, K = state.shape
+    B = mixed.shape[0]
+    out = np.empty((B, HV, V), np.float32)
+    a, b = _f32(a), _f32(b)
+    rc = lib().orc_packed_decode_float_state(
+        mixed, mixed.shape[1], a, a.shape[1], b, b.shape[1], _f32(A_log), _f32(dt_bias), float(scale),
+        state, state[0].size, int(bool(bf16)), out, np.ascontiguousarray(indices, np.int32), S,
+        B, H, HV, K, V, int(bool(use_qk_l2norm)))
+    if rc != 0:
+        raise ValueError("oracle: unsupported shape")
+    return out
 
 
 # ---------------------------------------------------------------------------

@@ -366,3 +366,263 @@ void orc_quantize_cols(const float* x, int64_t M, int K, int V, float qmax, int8
     }
   }
 }
+
+/* ------------------------------------------------------------------------- */
+/* Residual storage codecs of the statequant layout (statequant/kernel.py:    */
+/* 78-87): fp16 and fp8 e5m2 with round-to-nearest-even, written from the     */
+/* format definitions (sign | exponent | mantissa, subnormals, overflow to    */
+/* inf at and above the midpoint past the largest finite value).              */
+/* ------------------------------------------------------------------------- */
+uint16_t orc_f32_to_f16(float f) {
+  const uint32_t u = orc_float_to_bits(f);
+  const uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7e00u;       /* NaN */
+  if (a >= 0x477ff000u) return sign | 0x7c00u;      /* >= 65520 rounds to inf */
+  if (a < 0x38800000u) {                            /* below 2^-14: subnormal */
+    const float scaled = orc_bits_to_float(a) * 16777216.0f; /* x 2^24, exact */
+    return sign | (uint16_t)rintf(scaled);
+  }
+  const uint32_t lsb = (a >> 13) & 1u;
+  uint32_t r = (a + 0xfffu + lsb) >> 13;
+  r -= (127u - 15u) << 10;
+  return sign | (uint16_t)r;
+}
+
+float orc_f16_to_f32(uint16_t h) {
+  const uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  if (e == 0) {
+    const float v = (float)m * (1.0f / 16777216.0f); /* m x 2^-24, exact */
+    return sign ? -v : v;
+  }
+  if (e == 31) return orc_bits_to_float(sign | 0x7f800000u | (m << 13));
+  return orc_bits_to_float(sign | ((e - 15u + 127u) << 23) | (m << 13));
+}
+
+uint8_t orc_f32_to_e5m2(float f) {
+  const uint32_t u = orc_float_to_bits(f);
+  const uint8_t sign = (uint8_t)((u >> 24) & 0x80u);
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7fu;         /* NaN */
+  if (a >= 0x47700000u) return sign | 0x7cu;        /* >= 61440 rounds to inf */
+  if (a < 0x38800000u) {                            /* below 2^-14: subnormal */
+    const float scaled = orc_bits_to_float(a) * 65536.0f; /* x 2^16, exact */
+    return sign | (uint8_t)rintf(scaled);
+  }
+  const uint32_t lsb = (a >> 21) & 1u;
+  uint32_t r = (a + 0xfffffu + lsb) >> 21;
+  r -= (127u - 15u) << 2;
+  return sign | (uint8_t)r;
+}
+
+float orc_e5m2_to_f32(uint8_t b) {
+  const uint32_t sign = ((uint32_t)b & 0x80u) << 24;
+  const uint32_t e = (b >> 2) & 0x1fu, m = b & 3u;
+  if (e == 0) {
+    const float v = (float)m * (1.0f / 65536.0f);   /* m x 2^-16, exact */
+    return sign ? -v : v;
+  }
+  if (e == 31) return orc_bits_to_float(sign | 0x7f800000u | (m << 21));
+  return orc_bits_to_float(sign | ((e - 15u + 127u) << 23) | (m << 21));
+}
+
+void orc_f32_to_f16_n(const float* x, uint16_t* y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) y[i] = orc_f32_to_f16(x[i]);
+}
+void orc_f32_to_e5m2_n(const float* x, uint8_t* y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) y[i] = orc_f32_to_e5m2(x[i]);
+}
+void orc_e5m2_to_f32_n(const uint8_t* x, float* y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) y[i] = orc_e5m2_to_f32(x[i]);
+}
+
+/* ------------------------------------------------------------------------- */
+/* statequant layout: state [B, HV, K, V] (V contiguous), one scale per       */
+/* V-column (amax over K). K-reductions: the K rows split into 8 slices of    */
+/* K/8 consecutive rows; each slice is x0*y0 then fmaf over its rows; the 8   */
+/* slice sums combine as ((s0+s1)+(s2+s3))+((s4+s5)+(s6+s7)).                 */
+/* ------------------------------------------------------------------------- */
+#define RES_FP32 0
+#define RES_FP16 1
+#define RES_FP8 2
+#define RES_INT8 3
+
+static float dot_k8(const float* x, int64_t sx, const float* y, int K) {
+  float part[8];
+  const int rps = K / 8;
+  for (int sl = 0; sl < 8; ++sl) {
+    const int r0 = sl * rps;
+    float acc = x[(int64_t)r0 * sx] * y[r0];
+    for (int r = r0 + 1; r < r0 + rps; ++r) acc = fmaf(x[(int64_t)r * sx], y[r], acc);
+    part[sl] = acc;
+  }
+  return tree_sum(part, 8);
+}
+
+/* statequant/kernel.py:149-178 (torch reference) and :260-341 (GPU kernel):
+ * one out-of-place step. qmax applies to the state and to the int8 residual
+ * (the GPU kernels' convention, cuda/gdn_state_kernel.cu:210,233). */
+int orc_quant_step_kv(const int8_t* h_in, const float* scale_in, const void* e_in, const float* e_scale_in,
+                      const float* q, const float* k, const float* v, const float* alpha, const float* beta,
+                      float* o, int8_t* h_out, float* scale_out, void* e_out, float* e_scale_out,
+                      int B, int HV, int K, int V, float qmax, int res_fmt, int mode, int nthreads) {
+  if (K % 8 != 0 || K < 16) return 1;
+  (void)nthreads;
+#ifdef _OPENMP
+  if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel
+#endif
+  {
+    float* h = (float*)malloc(sizeof(float) * (size_t)K * V);
+    float* rd = (float*)malloc(sizeof(float) * V);
+    float* col = (float*)malloc(sizeof(float) * K);
+#ifdef _OPENMP
+#pragma omp for schedule(static)
+#endif
+    for (int64_t w = 0; w < (int64_t)B * HV; ++w) {
+      const int64_t mb = w * (int64_t)K * V, vb = w * V, kb = w * K;
+      const float a = alpha[w], bt = beta[w];
+      /* dequantize + decay (kernel.py:165-166) */
+      for (int r = 0; r < K; ++r)
+        for (int c = 0; c < V; ++c) {
+          const float code = (float)h_in[mb + (int64_t)r * V + c];
+          h[(int64_t)r * V + c] = mode == MODE_FAST ? code * (scale_in[vb + c] * a) : (code * scale_in[vb + c]) * a;
+        }
+      /* delta rule (kernel.py:167-170) */
+      for (int c = 0; c < V; ++c) rd[c] = bt * (v[vb + c] - dot_k8(h + c, V, k + kb, K));
+      for (int r = 0; r < K; ++r)
+        for (int c = 0; c < V; ++c) h[(int64_t)r * V + c] = madd(k[kb + r], rd[c], h[(int64_t)r * V + c], mode);
+      for (int c = 0; c < V; ++c) o[vb + c] = dot_k8(h + c, V, q + kb, K);
+      /* residual add (kernel.py:172) */
+      for (int r = 0; r < K; ++r)
+        for (int c = 0; c < V; ++c) {
+          const int64_t i = mb + (int64_t)r * V + c;
+          float* t = &h[(int64_t)r * V + c];
+          if (res_fmt == RES_INT8) {
+            *t = madd((float)((const int8_t*)e_in)[i], e_scale_in[vb + c], *t, mode);
+          } else if (res_fmt == RES_FP16) {
+            *t = *t + orc_f16_to_f32(((const uint16_t*)e_in)[i]);
+          } else if (res_fmt == RES_FP8) {
+            *t = *t + orc_e5m2_to_f32(((const uint8_t*)e_in)[i]);
+          } else {
+            *t = *t + ((const float*)e_in)[i];
+          }
+        }
+      /* requantize per V-column (kernel.py:173-177) */
+      for (int c = 0; c < V; ++c) {
+        float am = 0.0f;
+        for (int r = 0; r < K; ++r) am = fmaxf(am, fabsf(h[(int64_t)r * V + c]));
+        const float s = fmaxf(am / qmax, ORC_EPS);
+        const float inv = 1.0f / s;
+        float ea = 0.0f;
+        for (int r = 0; r < K; ++r) {
+          float* t = &h[(int64_t)r * V + c];
+          const float code = quant_code(*t, s, inv, qmax, mode);
+          h_out[mb + (int64_t)r * V + c] = (int8_t)code;
+          *t = resid_of(*t, code, s, mode); /* now the residual e' */
+          ea = fmaxf(ea, fabsf(*t));
+          col[r] = *t;
+        }
+        scale_out[vb + c] = s;
+        if (res_fmt == RES_INT8) {
+          const float es = fmaxf(ea / qmax, ORC_EPS);
+          const float inv_e = 1.0f / es;
+          for (int r = 0; r < K; ++r)
+            ((int8_t*)e_out)[mb + (int64_t)r * V + c] = (int8_t)quant_code(col[r], es, inv_e, qmax, mode);
+          e_scale_out[vb + c] = es;
+        } else {
+          for (int r = 0; r < K; ++r) {
+            const int64_t i = mb + (int64_t)r * V + c;
+            if (res_fmt == RES_FP16) ((uint16_t*)e_out)[i] = orc_f32_to_f16(col[r]);
+            else if (res_fmt == RES_FP8) ((uint8_t*)e_out)[i] = orc_f32_to_e5m2(col[r]);
+            else ((float*)e_out)[i] = col[r];
+          }
+        }
+      }
+    }
+    free(h);
+    free(rd);
+    free(col);
+  }
+  return 0;
+}
+
+/* FP32 GDN step in the statequant layout (statequant/kernel.py:116-123). */
+int orc_fp32_step_kv(const float* h_in, const float* q, const float* k, const float* v, const float* alpha,
+                     const float* beta, float* o, float* h_out, int B, int HV, int K, int V) {
+  if (K % 8 != 0 || K < 16) return 1;
+  float* rd = (float*)malloc(sizeof(float) * V);
+  for (int64_t w = 0; w < (int64_t)B * HV; ++w) {
+    const int64_t mb = w * (int64_t)K * V, vb = w * V, kb = w * K;
+    float* h = h_out + mb;
+    for (int64_t i = 0; i < (int64_t)K * V; ++i) h[i] = h_in[mb + i] * alpha[w];
+    for (int c = 0; c < V; ++c) rd[c] = beta[w] * (v[vb + c] - dot_k8(h + c, V, k + kb, K));
+    for (int r = 0; r < K; ++r)
+      for (int c = 0; c < V; ++c) h[(int64_t)r * V + c] = fmaf(k[kb + r], rd[c], h[(int64_t)r * V + c]);
+    for (int c = 0; c < V; ++c) o[vb + c] = dot_k8(h + c, V, q + kb, K);
+  }
+  free(rd);
+  return 0;
+}
+
+/* vLLM-layout step with an unquantized fp32 or bf16 state pool (the
+ * comparison arm): state [S, HV, V, K] as fp32 values; with bf16 != 0 the
+ * stored state is rounded to bf16 (nearest even) and kept as fp32 values. */
+static float bf16_round_f(float x) {
+  uint32_t u = orc_float_to_bits(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return x;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return orc_bits_to_float(u & 0xffff0000u);
+}
+
+int orc_packed_decode_float_state(const float* mixed, int64_t stride_mixed,
+                                  const float* a, int64_t stride_a, const float* b, int64_t stride_b,
+                                  const float* A_log, const float* dt_bias, float scale,
+                                  float* state, int64_t stride_state, int bf16,
+                                  float* out, const int32_t* idx, int64_t num_slots,
+                                  int B, int H, int HV, int K, int V, int l2norm) {
+  if (K % 16 != 0 || K > 256 || (K / 16 & (K / 16 - 1)) != 0 || HV % H != 0) return 1;
+  float* q = (float*)malloc(sizeof(float) * K);
+  float* k = (float*)malloc(sizeof(float) * K);
+  for (int64_t w = 0; w < (int64_t)B * HV; ++w) {
+    const int n = (int)(w / HV), hv = (int)(w % HV);
+    const int64_t slot = idx[n];
+    float* o = out + ((int64_t)n * HV + hv) * V;
+    if (slot <= 0 || slot >= num_slots) {
+      for (int r = 0; r < V; ++r) o[r] = slot <= 0 ? 0.0f : NAN;
+      continue;
+    }
+    const int hq = hv / (HV / H);
+    const float* m = mixed + (int64_t)n * stride_mixed;
+    for (int j = 0; j < K; ++j) {
+      q[j] = m[(int64_t)hq * K + j];
+      k[j] = m[(int64_t)H * K + (int64_t)hq * K + j];
+    }
+    if (l2norm) {
+      const float dq = sqrtf(dot_k(q, 1, q, 1, K) + 1e-6f);
+      const float dk = sqrtf(dot_k(k, 1, k, 1, K) + 1e-6f);
+      for (int j = 0; j < K; ++j) {
+        q[j] = q[j] / dq;
+        k[j] = k[j] / dk;
+      }
+    }
+    for (int j = 0; j < K; ++j) q[j] = q[j] * scale;
+    float alpha, beta;
+    orc_gates(a[(int64_t)n * stride_a + hv], b[(int64_t)n * stride_b + hv], A_log[hv], dt_bias[hv], &alpha, &beta);
+    float* st = state + slot * stride_state + (int64_t)hv * V * K;
+    const float* vv = m + 2 * (int64_t)H * K + (int64_t)hv * V;
+    for (int r = 0; r < V; ++r) {
+      float* h = st + (int64_t)r * K;
+      for (int j = 0; j < K; ++j) h[j] = h[j] * alpha;
+      const float dv = beta * (vv[r] - dot_k(h, 1, k, 1, K));
+      for (int j = 0; j < K; ++j) h[j] = fmaf(k[j], dv, h[j]);
+      o[r] = dot_k(h, 1, q, 1, K);
+      if (bf16)
+        for (int j = 0; j < K; ++j) h[j] = bf16_round_f(h[j]);
+    }
+  }
+  free(q);
+  free(k);
+  return 0;
+}
