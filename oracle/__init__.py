@@ -204,10 +204,12 @@ def f32_to_e5m2_bits(x) -> np.ndarray:
 
 
 def e5m2_bits_to_f32(b) -> np.ndarray:
-    b = np.ascontiguousarray(np.asarray(b, np.uint8))
-    y = np.empty(b.shape, np.float32)
-    lib().orc_e5m2_to_f32_n(b.ravel(), y.ravel(), b.size)
-    return y
+    b = np.asarray(b, np.uint8)
+    shape = b.shape
+    flat = np.ascontiguousarray(b.ravel())
+    y = np.empty(flat.shape, np.float32)
+    lib().orc_e5m2_to_f32_n(flat, y, flat.size)
+    return y.reshape(shape)
 
 
 def quant_step_kv(h_int8, scale, e, e_scale, q, k, v, alpha, beta, bits=8, res_fmt=RES_FP32,

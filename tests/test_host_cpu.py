@@ -1,0 +1,215 @@
+"""Host-side tests without a GPU: the C ABI library loads and exports every
+declared symbol, argument errors come back as status codes, the Python
+front ends raise the reference's errors, and nothing falls back to the CPU."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from carrykernel_amd import _native, build
+from carrykernel_amd.statequant import kernel as sq
+from carrykernel_amd.vllm_integration import quantized_packed_decode as qpd
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "carrykernel_gdn.h")
+
+
+def _declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(ck_\w+)\s*\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def L():
+    if not _native.library_available():
+        pytest.skip("library not built")
+    return _native.lib()
+
+
+def test_library_exports_every_declared_symbol(L):
+    declared = _declared_symbols()
+    assert len(declared) >= 8
+    raw = ctypes.CDLL(_native.LIB_PATH)
+    for name in declared:
+        assert hasattr(raw, name), f"{name} declared in include/carrykernel_gdn.h but not exported"
+    assert set(declared) == set(_native.exported_symbols())
+    assert L.ck_abi_version() == _native.ABI_VERSION
+
+
+def _pd_args(**over):
+    """Argument list of ck_gdn_packed_decode with dummy (never dereferenced) pointers."""
+    p = ctypes.c_void_p(16)
+    a = dict(mixed=p, qkv_dtype=0, stride_qkv=384, a=p, a_dtype=0, stride_a=2, b=p, b_dtype=0, stride_b=2,
+             A_log=p, A_log_dtype=0, dt_bias=p, dt_bias_dtype=0, scale=1.0,
+             state=p, stride_state=2 * 64 * 128, sscale=p, stride_sscale=128, resid=p,
+             stride_resid=2 * 64 * 64, rscale=p, stride_rscale=2, out=p, out_dtype=0, idx=p, stride_idx=1,
+             num_slots=4, B=1, H=1, HV=2, K=128, V=64, l2=0, resid_fmt=1, rscale_mode=1, bits=8, mode=0,
+             stream=None)
+    a.update(over)
+    return list(a.values())
+
+
+@pytest.mark.parametrize("over,status,msg", [
+    (dict(K=24), _native.CK_EUNSUPPORTED, "K must be one of"),
+    (dict(HV=3, H=2), _native.CK_EINVAL, "multiple of H"),
+    (dict(qkv_dtype=7), _native.CK_EINVAL, "dtype"),
+    (dict(resid_fmt=5), _native.CK_EINVAL, "resid_fmt"),
+    (dict(rscale_mode=9), _native.CK_EINVAL, "rscale_mode"),
+    (dict(mode=4), _native.CK_EINVAL, "quant_mode"),
+    (dict(bits=9), _native.CK_EINVAL, "state_bits"),
+    (dict(num_slots=0), _native.CK_EINVAL, "num_slots"),
+    (dict(mixed=None), _native.CK_EINVAL, "null pointer"),
+    (dict(state=ctypes.c_void_p(17)), _native.CK_EINVAL, "16-byte aligned"),
+    (dict(stride_state=-1), _native.CK_EINVAL, "aligned"),
+])
+def test_packed_decode_argument_errors(L, over, status, msg):
+    rc = L.ck_gdn_packed_decode(*_pd_args(**over))
+    assert rc == status
+    assert msg in L.ck_last_error().decode()
+
+
+def test_packed_decode_empty_batch_is_ok(L):
+    assert L.ck_gdn_packed_decode(*_pd_args(B=0)) == _native.CK_OK
+    assert L.ck_last_error().decode() == ""
+
+
+def test_other_entry_points_argument_errors(L):
+    p = ctypes.c_void_p(16)
+    rc = L.ck_gdn_quant_step(p, p, p, p, p, p, p, p, p, p, p, p, p, p, 1, 1, 24, 8, 127.0, 0, 0, None)
+    assert rc == _native.CK_EUNSUPPORTED and "K must be" in L.ck_last_error().decode()
+    rc = L.ck_gdn_quant_step(p, p, p, p, p, p, p, p, p, p, p, p, p, p, 1, 1, 32, 6, 127.0, 0, 0, None)
+    assert rc == _native.CK_EUNSUPPORTED and "multiple of 4" in L.ck_last_error().decode()
+    rc = L.ck_gdn_quant_step(p, p, p, p, p, p, p, p, p, p, p, p, p, p, 1, 1, 32, 8, 12.5, 0, 0, None)
+    assert rc == _native.CK_EINVAL and "qmax" in L.ck_last_error().decode()
+    rc = L.ck_gdn_quant_step(p, p, p, None, p, p, p, p, p, p, p, p, p, None, 1, 1, 32, 8, 127.0, 3, 0, None)
+    assert rc == _native.CK_EINVAL and "e_scale" in L.ck_last_error().decode()
+    rc = L.ck_gdn_fp32_step(p, p, p, p, p, p, p, p, 1, 1, 48, 8, None)
+    assert rc == _native.CK_EUNSUPPORTED
+    rc = L.ck_quantize_rows(p, 9, 128, 4, 128, 127.0, p, p, None)
+    assert rc == _native.CK_EINVAL
+    rc = L.ck_quantize_cols(p, 1, 32, 8, 300.0, p, p, None)
+    assert rc == _native.CK_EINVAL
+    rc = L.ck_gdn_packed_decode_float_state(p, 0, 384, p, 0, 2, p, 0, 2, p, 0, p, 0, 1.0, p, 2, 100, p, 0, p, 1,
+                                            4, 1, 1, 2, 128, 64, 0, None)
+    assert rc == _native.CK_EINVAL and "float32 or bfloat16" in L.ck_last_error().decode()
+
+
+# ---------------------------------------------------------------------------
+# Python front ends: the reference's ValueErrors (quantized_packed_decode.py:268-309)
+# ---------------------------------------------------------------------------
+
+def _cpu_case(B=2, H=2, HV=4, K=64, V=32, resid_fmt=qpd.RESID_INT4):
+    S = 3
+    rk = K // 2 if resid_fmt == qpd.RESID_INT4 else K
+    return dict(mixed_qkv=torch.zeros(B, 2 * H * K + HV * V), a=torch.zeros(B, HV), b=torch.zeros(B, HV),
+                A_log=torch.zeros(HV), dt_bias=torch.zeros(HV), scale=1.0,
+                state_codes=torch.zeros(S, HV, V, K, dtype=torch.int8), state_scale=torch.zeros(S, HV, V),
+                resid_codes=torch.zeros(S, HV, V, rk, dtype=torch.int8), resid_scale=torch.zeros(S, HV, V),
+                out=torch.zeros(B, 1, HV, V), ssm_state_indices=torch.tensor([1, 2], dtype=torch.int32),
+                resid_fmt=resid_fmt)
+
+
+@pytest.mark.parametrize("mutate,msg", [
+    (lambda c: c.update(mixed_qkv=torch.zeros(2, 3, 4)), "mixed_qkv must be 2-D"),
+    (lambda c: c.update(mixed_qkv=torch.zeros(512, 2).t()), "contiguous in its last dimension"),
+    (lambda c: c.update(state_codes=torch.zeros(3, 4, 32, dtype=torch.int8)), "state_codes must be 4-D"),
+    (lambda c: c.update(state_codes=torch.zeros(3, 4, 64, 32, dtype=torch.int8).transpose(2, 3)),
+     "state_codes must be contiguous in its last dimension"),
+    (lambda c: c.update(resid_codes=c["resid_codes"].float()), "must be int8 storage"),
+    (lambda c: c.update(resid_codes=torch.zeros(3, 4, 32, 64, dtype=torch.int8)), "packed two codes per byte"),
+    (lambda c: c.update(resid_fmt=qpd.RESID_INT8), "same shape as the state"),
+    (lambda c: c.update(ssm_state_indices=torch.tensor([[1, 2]], dtype=torch.int32)), "must be 1-D"),
+    (lambda c: c.update(ssm_state_indices=torch.tensor([1, 2])), "must be int32"),
+    (lambda c: c.update(out=torch.zeros(2, 4, 32)), "out must be"),
+    (lambda c: c.update(out=torch.zeros(2, 1, 32, 4).transpose(2, 3)), "out must be contiguous"),
+    (lambda c: c.update(mixed_qkv=torch.zeros(2, 4 * 32 + 1)), "cannot infer H"),
+    (lambda c: c.update(resid_scale=torch.zeros(3, 5)), "resid_scale must be"),
+    (lambda c: c.update(state_scale=torch.zeros(3, 4, 32, dtype=torch.float16)), "state_scale must be"),
+])
+def test_qpd_value_errors(mutate, msg):
+    c = _cpu_case()
+    mutate(c)
+    with pytest.raises(ValueError, match=re.escape(msg)):
+        qpd.quantized_gated_delta_rule_packed_decode(**c)
+
+
+def test_qpd_unsupported_k():
+    c = _cpu_case(K=48, resid_fmt=qpd.RESID_INT8)
+    with pytest.raises(ValueError, match="packed decode supports K"):
+        qpd.quantized_gated_delta_rule_packed_decode(**c)
+
+
+def test_qpd_no_cpu_fallback():
+    """Valid arguments on CPU tensors: the op refuses (HipUnavailable, a
+    RuntimeError) instead of computing anything on the host."""
+    with pytest.raises(_native.HipUnavailable):
+        qpd.quantized_gated_delta_rule_packed_decode(**_cpu_case())
+    with pytest.raises(_native.HipUnavailable):
+        qpd.init_quantized_state(2, 4, 32, 64, "cpu")
+    B, HV, K, V = 1, 2, 32, 8
+    z = torch.zeros
+    with pytest.raises(_native.HipUnavailable):
+        sq.gdn_quant_step_fused(z(B, HV, K, V, dtype=torch.int8), z(B, HV, V), z(B, HV, K, V), None, z(B, HV, K),
+                                z(B, HV, K), z(B, HV, V), z(B, HV), z(B, HV))
+    with pytest.raises(_native.HipUnavailable):
+        sq.gdn_step_fused_fp32(z(B, HV, K, V), z(B, HV, K), z(B, HV, K), z(B, HV, V), z(B, HV), z(B, HV))
+    with pytest.raises(_native.HipUnavailable):
+        sq.per_v_channel_quantize(z(2, K, V))
+
+
+def test_statequant_shape_errors():
+    B, HV, K, V = 1, 2, 32, 8
+    z = torch.zeros
+    with pytest.raises(AssertionError):
+        sq.gdn_quant_step_fused(z(B, HV, K, V), z(B, HV, V), z(B, HV, K, V), None, z(B, HV, K), z(B, HV, K),
+                                z(B, HV, V), z(B, HV), z(B, HV))
+    with pytest.raises(ValueError, match="e must be"):
+        sq.gdn_quant_step_fused(z(B, HV, K, V, dtype=torch.int8), z(B, HV, V), z(B, HV, K, V), None, z(B, HV, K),
+                                z(B, HV, K), z(B, HV, V), z(B, HV), z(B, HV), res_fmt=sq.RES_FP16)
+    with pytest.raises(ValueError, match="e_scale"):
+        sq.gdn_quant_step_fused(z(B, HV, K, V, dtype=torch.int8), z(B, HV, V), z(B, HV, K, V, dtype=torch.int8),
+                                None, z(B, HV, K), z(B, HV, K), z(B, HV, V), z(B, HV), z(B, HV),
+                                res_fmt=sq.RES_INT8)
+    with pytest.raises(ValueError, match="k must be"):
+        sq.gdn_quant_step_fused(z(B, HV, K, V, dtype=torch.int8), z(B, HV, V), z(B, HV, K, V), None, z(B, HV, K),
+                                z(B, HV, K + 1), z(B, HV, V), z(B, HV), z(B, HV))
+
+
+def test_debug_index_checks():
+    qpd._check_indices_host(torch.tensor([0, 2, 3, 0], dtype=torch.int32), 4)
+    with pytest.raises(ValueError, match="duplicate"):
+        qpd._check_indices_host(torch.tensor([1, 2, 1], dtype=torch.int32), 4)
+    with pytest.raises(ValueError, match=">= num_slots"):
+        qpd._check_indices_host(torch.tensor([1, 4], dtype=torch.int32), 4)
+
+
+def test_reference_constants():
+    """quantized_packed_decode.py:73-83 and statequant/kernel.py:56-66."""
+    assert (qpd.QMAX_INT8, qpd.QMAX_INT4, qpd.EPS, qpd.SOFTPLUS_THRESHOLD, qpd.NULL_BLOCK_ID) == (
+        127.0, 7.0, 1e-12, 20.0, 0)
+    assert (qpd.RESID_INT8, qpd.RESID_INT4) == (0, 1)
+    assert (sq.RES_FP32, sq.RES_FP16, sq.RES_FP8, sq.RES_INT8) == (0, 1, 2, 3)
+    assert [sq.residual_bytes(f) for f in range(4)] == [4, 2, 1, 1]
+    assert [sq.residual_label(f) for f in range(4)] == ["fp32", "fp16", "fp8", "int8"]
+    assert sq.residual_dtype(sq.RES_FP8) == torch.float8_e5m2
+
+
+def test_product_never_imports_the_oracle():
+    pkg = os.path.join(REPO, "carrykernel_amd")
+    for root, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".h", ".cpp")):
+                text = open(os.path.join(root, f)).read()
+                assert not re.search(r"^\s*(import|from)\s+oracle\b", text, re.M), f
+                assert "gdn_oracle" not in text, f
+
+
+def test_build_flags():
+    flags = " ".join(build.HIPCC_FLAGS)
+    assert "--offload-arch=gfx950" in flags
+    assert "-packed-fp32-ops" in flags and "-ffp-contract=off" in flags
