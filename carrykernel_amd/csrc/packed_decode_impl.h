@@ -294,17 +294,10 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
     }
   }
   __syncthreads();
-  float qq[16], kk[16];
-  {
-    const float4* q4 = reinterpret_cast<const float4*>(buf + c * 16);
-    const float4* k4 = reinterpret_cast<const float4*>(buf + K + c * 16);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float4 a4 = q4[j], b4 = k4[j];
-      qq[4 * j] = a4.x, qq[4 * j + 1] = a4.y, qq[4 * j + 2] = a4.z, qq[4 * j + 3] = a4.w;
-      kk[4 * j] = b4.x, kk[4 * j + 1] = b4.y, kk[4 * j + 2] = b4.z, kk[4 * j + 3] = b4.w;
-    }
-  }
+  // k and q are read from LDS for every row (not held in registers across
+  // rows): 32 fewer VGPRs, so more waves per SIMD hide latency.
+  const float4* q4 = reinterpret_cast<const float4*>(buf + c * 16);
+  const float4* k4 = reinterpret_cast<const float4*>(buf + K + c * 16);
 
   int8_t* sbase = p.state + ic.slot * p.stride_state + (int64_t)ic.hv * p.V * K;
   int8_t* ebase = p.resid + ic.slot * p.stride_resid + (int64_t)ic.hv * p.V * L::RK;
@@ -321,6 +314,13 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
     const int r = row0 + i * L::RPI;
     const bool valid = r < p.V;
     const uint32_t cws[4] = {R.cw[i].x, R.cw[i].y, R.cw[i].z, R.cw[i].w};
+    asm volatile("" ::: "memory");  // re-read k, q from LDS for this row
+    float kk[16], qq[16];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float4 b4 = k4[j];
+      kk[4 * j] = b4.x, kk[4 * j + 1] = b4.y, kk[4 * j + 2] = b4.z, kk[4 * j + 3] = b4.w;
+    }
 
     // dequantize + decay
     float h[16];
@@ -341,6 +341,11 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
     const float dv = beta * (act_from_raw(R.vv[i], p.mixed_dtype()) - rd);
 #pragma unroll
     for (int j = 0; j < 16; ++j) h[j] = madd<MODE>(kk[j], dv, h[j]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float4 a4 = q4[j];
+      qq[4 * j] = a4.x, qq[4 * j + 1] = a4.y, qq[4 * j + 2] = a4.z, qq[4 * j + 3] = a4.w;
+    }
     float o = h[0] * qq[0];
 #pragma unroll
     for (int j = 1; j < 16; ++j) o = fmaf(h[j], qq[j], o);
@@ -443,9 +448,14 @@ __device__ __forceinline__ void gates_for_items(const PackedParams& p, int kbase
   }
 }
 
+// Waves per SIMD the register allocation must allow: two 8-wave workgroups
+// per CU need 4 (<= 128 VGPRs); other shapes take what they need.
+template <int RPL, int WAVES>
+constexpr int kMinWavesPerEU = (RPL == 2 && WAVES == 8) ? 4 : 1;
+
 template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ESZ>
-__global__ __launch_bounds__(WAVES * 64) void packed_decode_kernel(const PackedParams p,
-                                                                   const int32_t* __restrict__ idx) {
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(kMinWavesPerEU<RPL, WAVES>)))
+void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx) {
   using L = Layout<K, RPL, WAVES, RESID, PER_HEAD>;
   __shared__ __attribute__((aligned(16))) float s_qk[4][2 * K];  // [parity] staged, [2 + parity] raw
   __shared__ float s_red[2][WAVES];
@@ -541,6 +551,8 @@ int launch_k(const PackedParams& p, int B, hipStream_t stream) {
     return launch_cfg<K, 4, 1, RESID, false, MODE, ESZ>(p, B, stream);
   } else {
     const int need = p.V;
+    if (K == 128 && need > RPI * 4 * 2 && need <= RPI * 2 * 8)
+      return launch_cfg<K, 2, 8, RESID, true, MODE, ESZ>(p, B, stream);
     if (need <= RPI * 4 * 1) return launch_cfg<K, 4, 1, RESID, true, MODE, ESZ>(p, B, stream);
     if (need <= RPI * 4 * 2) return launch_cfg<K, 4, 2, RESID, true, MODE, ESZ>(p, B, stream);
     if (need <= RPI * 4 * 4) return launch_cfg<K, 4, 4, RESID, true, MODE, ESZ>(p, B, stream);
