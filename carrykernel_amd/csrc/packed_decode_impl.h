@@ -435,17 +435,16 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
 // Gates of this workgroup's items number kbase .. kbase+63 (one per lane).
 __device__ __forceinline__ void gates_for_items(const PackedParams& p, int kbase, int lane, float& alpha_v,
                                                 float& beta_v) {
-  const int item = (int)blockIdx.x + (kbase + lane) * (int)gridDim.x;
-  alpha_v = 1.0f;
-  beta_v = 0.0f;
-  if (item < p.items) {
-    const uint32_t nh = fdiv((uint32_t)item, p.div_nvt);
-    const uint32_t n = fdiv(nh, p.div_hv);
-    const int hv = (int)(nh - n * p.div_hv.d);
-    ck_gates(load_act(p.a, (int64_t)n * p.stride_a + hv, p.a_dtype()),
-             load_act(p.b, (int64_t)n * p.stride_b + hv, p.b_dtype()), load_act(p.A_log, hv, p.A_log_dtype()),
-             load_act(p.dt_bias, hv, p.dt_bias_dtype()), &alpha_v, &beta_v);
-  }
+  // Branch-free over lanes (lanes past the last item recompute the last
+  // item's gates, which are never read): a divergent region here would move
+  // the uniform dtype/stride values into VGPRs that stay live over the loop.
+  const int item = min((int)blockIdx.x + (kbase + lane) * (int)gridDim.x, p.items - 1);
+  const uint32_t nh = fdiv((uint32_t)item, p.div_nvt);
+  const uint32_t n = fdiv(nh, p.div_hv);
+  const int hv = (int)(nh - n * p.div_hv.d);
+  ck_gates(load_act(p.a, (int64_t)n * p.stride_a + hv, p.a_dtype()),
+           load_act(p.b, (int64_t)n * p.stride_b + hv, p.b_dtype()), load_act(p.A_log, hv, p.A_log_dtype()),
+           load_act(p.dt_bias, hv, p.dt_bias_dtype()), &alpha_v, &beta_v);
 }
 
 // Waves per SIMD the register allocation must allow: two 8-wave workgroups
@@ -541,7 +540,10 @@ int launch_cfg(PackedParams p, int B, hipStream_t stream) {
 // Workgroup shape. K=128: a lane holds 4 rows, a wave 32 rows. With per-row
 // residual scales a workgroup is 4 waves (a whole 128-row head) when there are
 // enough heads to fill the GPU, else 1 wave (32-row tiles, 4x the items). A
-// per-head residual scale needs the whole head in one workgroup.
+// per-head residual scale needs the whole head in one workgroup; with the
+// packed int4 residual at K=128 that is 8 waves of 2 rows per lane, which fits
+// 128 VGPRs and so two workgroups per CU (int8 residual rows need more
+// registers and keep 4 rows per lane).
 template <int K, int RESID, bool PER_HEAD, int MODE, int ESZ>
 int launch_k(const PackedParams& p, int B, hipStream_t stream) {
   constexpr int RPI = 64 / (K / 16);
@@ -551,8 +553,9 @@ int launch_k(const PackedParams& p, int B, hipStream_t stream) {
     return launch_cfg<K, 4, 1, RESID, false, MODE, ESZ>(p, B, stream);
   } else {
     const int need = p.V;
-    if (K == 128 && need > RPI * 4 * 2 && need <= RPI * 2 * 8)
-      return launch_cfg<K, 2, 8, RESID, true, MODE, ESZ>(p, B, stream);
+    if constexpr (K == 128 && RESID == kResidInt4) {
+      if (need > RPI * 4 * 2 && need <= RPI * 2 * 8) return launch_cfg<K, 2, 8, RESID, true, MODE, ESZ>(p, B, stream);
+    }
     if (need <= RPI * 4 * 1) return launch_cfg<K, 4, 1, RESID, true, MODE, ESZ>(p, B, stream);
     if (need <= RPI * 4 * 2) return launch_cfg<K, 4, 2, RESID, true, MODE, ESZ>(p, B, stream);
     if (need <= RPI * 4 * 4) return launch_cfg<K, 4, 4, RESID, true, MODE, ESZ>(p, B, stream);
