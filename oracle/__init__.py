@@ -83,6 +83,8 @@ def lib():
             L.orc_f32_to_e5m2_n.argtypes = [_f32p, _u8p, _i64]
             L.orc_e5m2_to_f32_n.argtypes = [_u8p, _f32p, _i64]
             L.orc_quantize_cols.argtypes = [_f32p, _i64, _int, _int, _flt, _i8p, _f32p]
+            L.orc_count_div_small_int_mismatches.restype = _i64
+            L.orc_count_div_small_int_mismatches.argtypes = [_flt, _int, _int]
             _lib = L
     return _lib
 
@@ -316,3 +318,9 @@ def gdn_step_f64(h, q, k, v, alpha, beta):
     h = h + k[..., :, None] * dv[..., None, :]
     o = np.einsum("...kv,...k->...v", h, q)
     return h, o
+
+
+def count_div_small_int_mismatches(q: float, e_lo: int, e_hi: int) -> int:
+    """Mismatches of the kernels' Markstein quotient RN(a/q) against IEEE a/q
+    over every mantissa of a at biased exponents e_lo..e_hi."""
+    return int(lib().orc_count_div_small_int_mismatches(float(q), int(e_lo), int(e_hi)))

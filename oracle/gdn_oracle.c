@@ -626,3 +626,27 @@ int orc_packed_decode_float_state(const float* mixed, int64_t stride_mixed,
   free(k);
   return 0;
 }
+
+/*
+ * Checker for the HIP kernels' scale division (not part of the step): the
+ * kernels compute RN(a / q) for a small integer q as Markstein's correction
+ * of the reciprocal product, q0 = RN(a * rq), r = fma(-q0, q, a),
+ * RN(fma(r, rq, q0)) with rq = RN(1 / q). Counts, over every mantissa of a at
+ * biased exponents e_lo..e_hi, the cases where that differs from the IEEE
+ * quotient a / q.
+ */
+int64_t orc_count_div_small_int_mismatches(float q, int e_lo, int e_hi) {
+  const float rq = 1.0f / q;
+  int64_t bad = 0;
+  for (int e = e_lo; e <= e_hi; ++e) {
+#pragma omp parallel for reduction(+ : bad)
+    for (int64_t m = 0; m < (1 << 23); ++m) {
+      const float a = orc_bits_to_float(((uint32_t)e << 23) | (uint32_t)m);
+      const float q0 = a * rq;
+      const float r = fmaf(-q0, q, a);
+      const float got = fmaf(r, rq, q0);
+      bad += orc_float_to_bits(got) != orc_float_to_bits(a / q);
+    }
+  }
+  return bad;
+}

@@ -74,6 +74,21 @@ def test_gates_match_closed_form():
 
 
 # ---------------------------------------------------------------------------
+# scale division of the kernels (amax / qmax without an IEEE divide)
+# ---------------------------------------------------------------------------
+
+def test_small_int_division_is_correctly_rounded():
+    """The kernels' RN(amax / qmax) (a Markstein-corrected reciprocal product)
+    equals the IEEE quotient for every qmax the kernels use (1..127) over all
+    mantissas at exponents from the 1e-12 eps floor to the top of the range."""
+    bad = sum(oracle.count_div_small_int_mismatches(q, e, e) for q in range(1, 128) for e in (87, 127, 200, 254))
+    assert bad == 0
+    # the checker discriminates: the uncorrected product RN(a * RN(1/q)) is wrong often
+    a = ((np.uint32(127) << 23) | np.arange(1 << 23, dtype=np.uint32)).view(F)
+    assert np.count_nonzero(a * (F(1) / F(3)) != a / F(3)) > 1000
+
+
+# ---------------------------------------------------------------------------
 # storage codecs
 # ---------------------------------------------------------------------------
 
