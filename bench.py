@@ -234,6 +234,90 @@ def copy_peak(device, mib, reps):
             "GBps": round(moved / (ms * 1e-3) / 1e9, 1)}
 
 
+def float_state_step(state, mixed, a, b, A_log, dt_bias, scale, out, idx, l2norm):
+    """One step of the unquantized fp32 state arm (ck_gdn_packed_decode_float_state)."""
+    from carrykernel_amd import _native
+    S, hv, v, k = state.shape
+    st = _native.lib().ck_gdn_packed_decode_float_state(
+        mixed.data_ptr(), 0, mixed.stride(0), a.data_ptr(), 0, a.stride(0), b.data_ptr(), 0, b.stride(0),
+        A_log.data_ptr(), 0, dt_bias.data_ptr(), 0, float(scale), state.data_ptr(), 0, state.stride(0),
+        out.data_ptr(), 0, idx.data_ptr(), idx.stride(0), S, mixed.shape[0], (mixed.shape[1] - hv * v) // (2 * k),
+        hv, k, v, int(l2norm),
+        _native.stream_handle(state.device))
+    _native.check(st, "float-state step")
+
+
+def dequant_pool(pool, resid_fmt, with_residual):
+    """codes * scale (+ the dequantized residual) of a vLLM pool, fp32 [S, HV, V, K]."""
+    sc, ss, rc, rs = pool
+    h = sc.float() * ss[..., None]
+    if not with_residual:
+        return h
+    if resid_fmt == qpd.RESID_INT4:
+        x = rc.to(torch.int32) & 0xFF
+        lo = ((x & 0xF) ^ 8) - 8
+        hi = ((x >> 4) ^ 8) - 8
+        e = torch.stack([lo, hi], dim=-1).reshape(*rc.shape[:-1], 2 * rc.shape[-1]).float()
+    else:
+        e = rc.float()
+    es = rs[..., None, None] if rs.dim() == 2 else rs[..., None]
+    return h + e * es
+
+
+def drift_c5(device, bits, tokens=2048, layers=24, B=64, every=256, resid_fmt=None, per_head=True,
+             seed=0, log=None):
+    """Config C5: `layers` GDN layers per token at batch B, fresh q/k/v per layer
+    and token, heads 0..HV/2-1 at alpha 0.995 and the rest at 0.9, beta =
+    sigmoid(U(-2, 2)), q/k L2-normalised in the kernel. The quantized pool
+    (int8 or int6 state, int4 residual with a per-head scale by default) and an
+    unquantized fp32 pool (the float-state arm, on the GPU) start from zero and
+    see identical inputs. Every `every` tokens: relative error of the
+    dequantized state (codes*scale, and with the residual added back) and of
+    the outputs, over all layers and requests."""
+    resid_fmt = qpd.RESID_INT4 if resid_fmt is None else resid_fmt
+    gen = torch.Generator(device=device).manual_seed(seed)
+    S = B + 1
+    idx = torch.arange(1, S, dtype=torch.int32, device=device)
+    pools = [qpd.init_quantized_state(S, HV, V, K, device, resid_fmt=resid_fmt, per_head_resid_scale=per_head,
+                                      state_bits=bits) for _ in range(layers)]
+    refs = [torch.zeros(S, HV, V, K, device=device) for _ in range(layers)]
+    alpha = torch.tensor([0.995] * (HV // 2) + [0.9] * (HV - HV // 2), dtype=torch.float64)
+    a = torch.log(torch.expm1(-torch.log(alpha))).float().to(device).expand(B, HV).contiguous()
+    A_log = torch.zeros(HV, device=device)
+    dt_bias = torch.zeros(HV, device=device)
+    out_q = torch.empty(B, 1, HV, V, device=device)
+    out_r = torch.empty(B, 1, HV, V, device=device)
+    width = 2 * H * K + HV * V
+    rows = []
+    for t in range(tokens):
+        report = (t + 1) % every == 0 or t == tokens - 1
+        do2 = dn2 = 0.0
+        for layer in range(layers):
+            mixed = torch.randn(B, width, generator=gen, device=device)
+            b = torch.rand(B, HV, generator=gen, device=device) * 4.0 - 2.0
+            qpd.quantized_gated_delta_rule_packed_decode(
+                mixed, a, b, A_log, dt_bias, 1.0, *pools[layer], out_q, idx, use_qk_l2norm_in_kernel=True,
+                resid_fmt=resid_fmt, state_bits=bits)
+            float_state_step(refs[layer], mixed, a, b, A_log, dt_bias, 1.0, out_r, idx, True)
+            if report:
+                do2 += float((out_q - out_r).double().square().sum())
+                dn2 += float(out_r.double().square().sum())
+        if report:
+            dh2 = dhe2 = hn2 = 0.0
+            for layer in range(layers):
+                ref = refs[layer][1:].double()
+                dh2 += float((dequant_pool(pools[layer], resid_fmt, False)[1:].double() - ref).square().sum())
+                dhe2 += float((dequant_pool(pools[layer], resid_fmt, True)[1:].double() - ref).square().sum())
+                hn2 += float(ref.square().sum())
+            row = {"token": t + 1, "state_rel": round(math.sqrt(dh2 / hn2), 6),
+                   "state_plus_residual_rel": round(math.sqrt(dhe2 / hn2), 6),
+                   "o_rel": round(math.sqrt(do2 / dn2), 6)}
+            rows.append(row)
+            if log:
+                log(row)
+    return rows
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -246,6 +330,10 @@ def main():
     ap.add_argument("--quant-mode", choices=("fast", "exact"), default="fast")
     ap.add_argument("--sweep", action="store_true", help="also time B in {1, 8, 64, 256} and variants")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--drift", action="store_true",
+                    help="instead: config C5 drift (24 layers x B=64 x 2048 tokens, int8 and int6 state) "
+                         "against the fp32 state arm; prints one JSON line")
+    ap.add_argument("--drift-tokens", type=int, default=2048)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="instead: time a plain device copy of this many MiB (HBM copy peak, and the "
@@ -262,6 +350,17 @@ def main():
     device = torch.device("cuda", 0)
     if args.copy_mib:
         print(json.dumps(copy_peak(device, args.copy_mib, args.steps)), flush=True)
+        return
+    if args.drift:
+        res = {}
+        for bits in (8, 6):
+            t0 = time.perf_counter()
+            rows = drift_c5(device, bits, tokens=args.drift_tokens,
+                            log=lambda r, bits=bits: print(f"int{bits}", json.dumps(r), file=sys.stderr, flush=True))
+            res[f"int{bits}"] = {"rows": rows, "seconds": round(time.perf_counter() - t0, 1)}
+        print(json.dumps({"config": "C5: 24 layers x B=64 x HV=32 x K=V=128, int4 residual (per-head scale), "
+                                    "alpha 0.995 (heads 0-15) / 0.9 (16-31), drift vs the fp32 state arm",
+                          "tokens": args.drift_tokens, "drift": res}), flush=True)
         return
     resid_fmt = qpd.RESID_INT4 if args.resid == "int4" else qpd.RESID_INT8
     per_head = args.rscale == "head"
@@ -302,9 +401,11 @@ def main():
             line["roofline"]["traffic"] = json.load(f).get("traffic_bytes_per_launch")
     if args.sweep:
         sweep = {}
-        for bb in (1, 8, 64, 256):
+        for bb in (1, 8, 64, 128, 256):   # B=128 int4 per-row: config C4's step
             for fmt_name, fmt, ph in (("int4_head", qpd.RESID_INT4, True), ("int4_row", qpd.RESID_INT4, False),
                                       ("int8_head", qpd.RESID_INT8, True), ("int8_row", qpd.RESID_INT8, False)):
+                if bb == 128 and fmt_name != "int4_row":
+                    continue
                 groups = max(2, min(64, 1024 // bb))
                 m, hm = run_config(device, bb, fmt, ph, max(200, args.steps // 4), 50, groups, args.quant_mode)
                 nb = algorithmic_bytes(bb, H, HV, K, V, fmt, ph)
