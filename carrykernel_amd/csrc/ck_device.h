@@ -48,7 +48,9 @@ __device__ __forceinline__ uint32_t load_act_raw(const char* base, uint32_t off)
   }
 }
 
+template <int ESZ>
 __device__ __forceinline__ float act_from_raw(uint32_t raw, int dtype) {
+  if constexpr (ESZ == 4) return __uint_as_float(raw);  // 4-byte activations are fp32
   if (dtype == kF32) return __uint_as_float(raw);
   if (dtype == kBF16) return __uint_as_float(raw << 16);
   _Float16 h;

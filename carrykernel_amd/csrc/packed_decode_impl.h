@@ -220,7 +220,7 @@ __device__ __forceinline__ void store_resid(int8_t* dst, const uint32_t (&eb)[16
 }
 
 // Compute and store one item whose registers are loaded.
-template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE>
+template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ESZ>
 __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCoord& ic, int row0, int c, int lane,
                                              int wave, int parity, float alpha, float beta,
                                              const ItemRegs<RPL, Layout<K, RPL, WAVES, RESID, PER_HEAD>::EW,
@@ -252,7 +252,7 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
 #pragma unroll
     for (int j = 0; j < L::QKT; ++j) {
       const int e = (int)threadIdx.x + j * L::NT;
-      if (e < 2 * K) raw[e] = act_from_raw(R.qk[j], p.mixed_dtype());
+      if (e < 2 * K) raw[e] = act_from_raw<ESZ>(R.qk[j], p.mixed_dtype());
     }
     __syncthreads();
     float sq, sk;
@@ -288,7 +288,7 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
     for (int j = 0; j < L::QKT; ++j) {
       const int e = (int)threadIdx.x + j * L::NT;
       if (e < 2 * K) {
-        const float x = act_from_raw(R.qk[j], p.mixed_dtype());
+        const float x = act_from_raw<ESZ>(R.qk[j], p.mixed_dtype());
         buf[e] = (e < K) ? x * p.scale : x;
       }
     }
@@ -338,7 +338,7 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
 #pragma unroll
     for (int j = 1; j < 16; ++j) rd = fmaf(h[j], kk[j], rd);
     rd = group_sum<LPR>(rd);
-    const float dv = beta * (act_from_raw(R.vv[i], p.mixed_dtype()) - rd);
+    const float dv = beta * (act_from_raw<ESZ>(R.vv[i], p.mixed_dtype()) - rd);
 #pragma unroll
     for (int j = 0; j < 16; ++j) h[j] = madd<MODE>(kk[j], dv, h[j]);
 #pragma unroll
@@ -350,6 +350,7 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
 #pragma unroll
     for (int j = 1; j < 16; ++j) o = fmaf(h[j], qq[j], o);
     o = group_sum<LPR>(o);
+    asm volatile("" : "+v"(o));  // finish the sum here, where its DPP steps fuse into adds
     if (c == 0 && valid) store_act_at(obase, (uint32_t)r, odt, o);
 
     // add the carried residual: t = h + e_code * e_scale
@@ -487,7 +488,7 @@ void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx)
     {
       const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), k & 63));
       const float beta = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(beta_v), k & 63));
-      process_item<K, RPL, WAVES, RESID, PER_HEAD, MODE>(p, ca, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c,
+      process_item<K, RPL, WAVES, RESID, PER_HEAD, MODE, ESZ>(p, ca, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c,
                                                           lane, wave, live & 1, alpha, beta, A, s_qk, s_red);
       live += ca.live ? 1 : 0;
     }
@@ -503,7 +504,7 @@ void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx)
     {
       const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), k & 63));
       const float beta = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(beta_v), k & 63));
-      process_item<K, RPL, WAVES, RESID, PER_HEAD, MODE>(p, cb, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c,
+      process_item<K, RPL, WAVES, RESID, PER_HEAD, MODE, ESZ>(p, cb, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c,
                                                           lane, wave, live & 1, alpha, beta, B, s_qk, s_red);
       live += cb.live ? 1 : 0;
     }
