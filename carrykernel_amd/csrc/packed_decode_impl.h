@@ -448,10 +448,11 @@ __device__ __forceinline__ void gates_for_items(const PackedParams& p, int kbase
            load_act(p.dt_bias, hv, p.dt_bias_dtype()), &alpha_v, &beta_v);
 }
 
-// Waves per SIMD the register allocation must allow: two 8-wave workgroups
-// per CU need 4 (<= 128 VGPRs); other shapes take what they need.
+// Waves per SIMD the register allocation must allow: two 8-wave or four
+// 4-wave workgroups per CU need 4 (<= 128 VGPRs); other shapes take what they
+// need.
 template <int RPL, int WAVES>
-constexpr int kMinWavesPerEU = (RPL == 2 && WAVES == 8) ? 4 : 1;
+constexpr int kMinWavesPerEU = (RPL == 2 && (WAVES == 8 || WAVES == 4)) ? 4 : 1;
 
 template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ESZ>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(kMinWavesPerEU<RPL, WAVES>)))
@@ -538,9 +539,10 @@ int launch_cfg(PackedParams p, int B, hipStream_t stream) {
   return check_launch("ck_gdn_packed_decode");
 }
 
-// Workgroup shape. K=128: a lane holds 4 rows, a wave 32 rows. With per-row
-// residual scales a workgroup is 4 waves (a whole 128-row head) when there are
-// enough heads to fill the GPU, else 1 wave (32-row tiles, 4x the items). A
+// Workgroup shape (numbers for K=128, where a lane row is 16 K and a wave
+// instruction covers 8 rows). With per-row residual scales a workgroup is 4
+// waves of 2 rows per lane (64-row tiles, four workgroups per CU) when that
+// gives 512 tiles or more, else 1 wave of 4 rows per lane (32-row tiles). A
 // per-head residual scale needs the whole head in one workgroup; with the
 // packed int4 residual at K=128 that is 8 waves of 2 rows per lane, which fits
 // 128 VGPRs and so two workgroups per CU (int8 residual rows need more
@@ -549,8 +551,8 @@ template <int K, int RESID, bool PER_HEAD, int MODE, int ESZ>
 int launch_k(const PackedParams& p, int B, hipStream_t stream) {
   constexpr int RPI = 64 / (K / 16);
   if constexpr (!PER_HEAD) {
-    if ((int64_t)B * p.HV * ((p.V + RPI * 16 - 1) / (RPI * 16)) >= 512)
-      return launch_cfg<K, 4, 4, RESID, false, MODE, ESZ>(p, B, stream);
+    if ((int64_t)B * p.HV * ((p.V + RPI * 8 - 1) / (RPI * 8)) >= 512)
+      return launch_cfg<K, 2, 4, RESID, false, MODE, ESZ>(p, B, stream);
     return launch_cfg<K, 4, 1, RESID, false, MODE, ESZ>(p, B, stream);
   } else {
     const int need = p.V;
