@@ -84,12 +84,14 @@ _SIGNATURES = {
 
 
 def library_available() -> bool:
-    return os.path.exists(LIB_PATH)
+    return _lib is not None or os.path.exists(LIB_PATH)
 
 
 def lib():
     """Load (once) and return the ctypes handle; raises HipUnavailable."""
     global _lib
+    if _lib is not None:
+        return _lib
     with _lock:
         if _lib is None:
             if not os.path.exists(LIB_PATH):
@@ -118,8 +120,21 @@ def require_gpu(t: torch.Tensor, name: str) -> None:
             f"{name} is on {t.device}; the HIP kernels need GPU tensors (there is no CPU path)")
 
 
-def stream_handle(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def stream_handle(device) -> int:
+    """hipStream_t of torch's current stream on `device` (a torch.device or
+    a device index)."""
+    if isinstance(device, int):
+        index = device
+    else:
+        index = torch.device(device).index
+        if index is None:
+            index = torch.cuda.current_device()
+    if _raw_stream is not None:
+        return _raw_stream(index)
+    return torch.cuda.current_stream(index).cuda_stream
 
 
 def check(status: int, what: str) -> None:

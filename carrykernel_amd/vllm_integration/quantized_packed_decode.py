@@ -184,15 +184,16 @@ def quantized_gated_delta_rule_packed_decode(
     if not 2 <= int(state_bits) <= 8:
         raise ValueError(f"state_bits must be in 2..8, got {state_bits}")
 
-    dev = state_codes.device
+    dev = state_codes.get_device()   # -1 for a CPU tensor
     tensors = (("mixed_qkv", mixed_qkv), ("a", a), ("b", b), ("A_log", A_log),
                ("dt_bias", dt_bias), ("state_codes", state_codes), ("state_scale", state_scale),
                ("resid_codes", resid_codes), ("resid_scale", resid_scale), ("out", out),
                ("ssm_state_indices", ssm_state_indices))
     for name, t in tensors:
-        _native.require_gpu(t, name)
-        if t.device != dev:
-            raise ValueError(f"{name} is on {t.device}, the state pool on {dev}")
+        if t.get_device() != dev or dev < 0:
+            _native.require_gpu(t, name)
+            _native.require_gpu(state_codes, "state_codes")
+            raise ValueError(f"{name} is on {t.device}, the state pool on {state_codes.device}")
     if _DEBUG:
         _check_indices_host(ssm_state_indices[:B], num_slots)
 
