@@ -328,8 +328,11 @@ def main():
     ap.add_argument("--resid", choices=("int4", "int8"), default="int4")
     ap.add_argument("--rscale", choices=("head", "row"), default="head")
     ap.add_argument("--quant-mode", choices=("fast", "exact"), default="fast")
-    ap.add_argument("--sweep", action="store_true", help="also time B in {1, 8, 64, 256} and variants")
+    ap.add_argument("--sweep", action="store_true",
+                    help="time every B in {1, 8, 64, 256} x residual format x scale granularity (default: "
+                         "the headline format at B in {1, 8, 64, 256} and the C2 / C4 steps)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-sweep", action="store_true", help="time only the headline configuration")
     ap.add_argument("--drift", action="store_true",
                     help="instead: config C5 drift (24 layers x B=64 x 2048 tokens, int8 and int6 state) "
                          "against the fp32 state arm; prints one JSON line")
@@ -399,20 +402,32 @@ def main():
     if os.path.exists(traffic_path):
         with open(traffic_path) as f:
             line["roofline"]["traffic"] = json.load(f).get("traffic_bytes_per_launch")
-    if args.sweep:
-        sweep = {}
-        for bb in (1, 8, 64, 128, 256):   # B=128 int4 per-row: config C4's step
-            for fmt_name, fmt, ph in (("int4_head", qpd.RESID_INT4, True), ("int4_row", qpd.RESID_INT4, False),
-                                      ("int8_head", qpd.RESID_INT8, True), ("int8_row", qpd.RESID_INT8, False)):
-                if bb == 128 and fmt_name != "int4_row":
-                    continue
-                groups = max(2, min(64, 1024 // bb))
-                m, hm = run_config(device, bb, fmt, ph, max(200, args.steps // 4), 50, groups, args.quant_mode)
-                nb = algorithmic_bytes(bb, H, HV, K, V, fmt, ph)
-                sweep[f"B{bb}_{fmt_name}"] = {"us": round(m * 1e3, 3), "host_us": round(hm * 1e3, 3),
-                                             "GBps": round(nb / (m * 1e-3) / 1e9, 1),
-                                             "frac": round(nb / (m * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
-        line["sweep"] = sweep
+    # batch sweep of the same format (config C3), plus config C2's (B=8, int8
+    # residual, per-head scale) and C4's (B=128, int4, per-row scale) steps;
+    # --sweep adds every batch x residual format x scale granularity
+    formats = {"int4_head": (qpd.RESID_INT4, True), "int4_row": (qpd.RESID_INT4, False),
+               "int8_head": (qpd.RESID_INT8, True), "int8_row": (qpd.RESID_INT8, False)}
+    if args.no_sweep:
+        cases = []
+    elif args.sweep:
+        cases = [(bb, f) for bb in (1, 8, 64, 256) for f in formats] + [(128, "int4_row")]
+    else:
+        cases = [(bb, "int4_head") for bb in (1, 8, 256)] + [(8, "int8_head"), (128, "int4_row")]
+    sweep = {}
+    if args.batch == 64 and args.resid == "int4" and args.rscale == "head":
+        sweep["B64_int4_head"] = {"us": line["us_per_step"], "host_us": line["host_us_per_eager_call"],
+                                  "GBps": line["value"], "frac": line["roofline"]["frac"]}
+    for bb, fmt_name in cases:
+        if f"B{bb}_{fmt_name}" in sweep:
+            continue
+        fmt, ph = formats[fmt_name]
+        groups = max(2, min(64, 1024 // bb))
+        m, hm = run_config(device, bb, fmt, ph, max(200, args.steps // 4), 50, groups, args.quant_mode)
+        nb = algorithmic_bytes(bb, H, HV, K, V, fmt, ph)
+        sweep[f"B{bb}_{fmt_name}"] = {"us": round(m * 1e3, 3), "host_us": round(hm * 1e3, 3),
+                                     "GBps": round(nb / (m * 1e-3) / 1e9, 1),
+                                     "frac": round(nb / (m * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+    line["sweep"] = dict(sorted(sweep.items(), key=lambda kv: (int(kv[0][1:kv[0].index("_")]), kv[0])))
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(B, resid_fmt, per_head, args.cpu_seconds)
     print(json.dumps(line), flush=True)
