@@ -38,6 +38,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 if HERE not in sys.path:
     sys.path.insert(0, HERE)
 
+from carrykernel_amd.statequant import kernel as sq  # noqa: E402
 from carrykernel_amd.vllm_integration import quantized_packed_decode as qpd  # noqa: E402
 
 HBM_PEAK_GBPS = 8000.0
@@ -61,10 +62,15 @@ def algorithmic_bytes(B, H, HV, K, V, resid_fmt, per_head, act_bytes=4):
     return B * (HV * per_vhead + H * per_qkhead + 4)
 
 
+def float_state_bytes(B, H, HV, K, V, esz, act_bytes=4):
+    """Same step with an unquantized state of `esz` bytes per element."""
+    per_vhead = 2 * esz * K * V + 2 * act_bytes * V + 2 * act_bytes
+    return B * (HV * per_vhead + H * 2 * act_bytes * K + 4)
+
+
 def bf16_state_bytes(B, H, HV, K, V, act_bytes=4):
     """Same step with vLLM's default bf16 state (the comparison arm)."""
-    per_vhead = 2 * 2 * K * V + 2 * act_bytes * V + 2 * act_bytes
-    return B * (HV * per_vhead + H * 2 * act_bytes * K + 4)
+    return float_state_bytes(B, H, HV, K, V, 2, act_bytes)
 
 
 def make_step_inputs(B, n_sets, device, seed):
@@ -216,6 +222,127 @@ def run_config(device, B, resid_fmt, per_head, steps, warmup, groups, quant_mode
     return ms, host_ms
 
 
+def _graph_time(device, step, n_steps, warmup, reps_cap=None):
+    """Device ms per step of `step(t)` captured as n_steps consecutive launches
+    in one HIP graph and replayed (warm-up replays first)."""
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        for t in range(n_steps):
+            step(t)
+    torch.cuda.current_stream(device).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        for t in range(n_steps):
+            step(t)
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    reps = reps_cap or 20
+    timer = Timer(device)
+    timer.start()
+    for _ in range(reps):
+        graph.replay()
+    ms = timer.stop_ms() / (reps * n_steps)
+    del graph
+    return ms
+
+
+def statequant_bytes(B, HV, K, V, res_fmt):
+    """Unique bytes of one statequant-layout step (statequant/kernel.py:379-408):
+    int8 codes in/out, residual in/out, per-column state scale in/out (and the
+    int8 residual's per-column scale in/out), q/k/v/o fp32, alpha/beta."""
+    rb = {sq.RES_FP32: 4, sq.RES_FP16: 2, sq.RES_FP8: 1, sq.RES_INT8: 1}[res_fmt]
+    per = 2 * K * V + 2 * K * V * rb + 2 * 4 * V + (2 * 4 * V if res_fmt == sq.RES_INT8 else 0)
+    per += 2 * 4 * K + 2 * 4 * V + 2 * 4
+    return B * HV * per
+
+
+def arms(device, batches=(8, 64), steps=200):
+    """The other entry points at config shapes (HV=32, K=V=128, fp32
+    activations): the statequant-layout step for each residual format, its fp32
+    baseline, and the unquantized fp32 / bf16 state arms of the vLLM-layout
+    decode. Out-of-place steps ping-pong between buffer sets whose total exceeds
+    the 256 MB MALL. Returns {name: {us, GBps, frac}}."""
+    from carrykernel_amd import _native
+    L = _native.lib()
+    res = {}
+    gen = torch.Generator(device=device).manual_seed(3)
+
+    def rec(name, ms, nbytes):
+        res[name] = {"us": round(ms * 1e3, 3), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                     "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+
+    for B in batches:
+        q = torch.randn(B, HV, K, device=device, generator=gen)
+        k = torch.randn(B, HV, K, device=device, generator=gen)
+        k = k / k.norm(dim=-1, keepdim=True)
+        v = torch.randn(B, HV, V, device=device, generator=gen)
+        al = torch.full((B, HV), 0.99, device=device)
+        be = torch.full((B, HV), 0.5, device=device)
+        o = torch.empty(B, HV, V, device=device)
+        for res_fmt in (sq.RES_FP32, sq.RES_FP16, sq.RES_FP8, sq.RES_INT8):
+            per_set = B * HV * K * V * (1 + sq.residual_bytes(res_fmt))
+            nsets = max(2, min(64, -(-(512 << 20) // per_set)))
+            h0 = torch.randn(B, HV, K, V, device=device, generator=gen) * 0.1
+            sets = []
+            for _ in range(nsets):
+                hs = sq.init_quant_state(h0, 8, res_fmt)
+                es = hs[3] if hs[3] is not None else torch.zeros(B, HV, V, device=device)
+                sets.append((hs[0], hs[1], hs[2], es))
+            del h0
+
+            def step(t, sets=sets, res_fmt=res_fmt):
+                a_, b_ = sets[t % nsets], sets[(t + 1) % nsets]
+                st = L.ck_gdn_quant_step(a_[0].data_ptr(), a_[1].data_ptr(), a_[2].data_ptr(), a_[3].data_ptr(),
+                                         q.data_ptr(), k.data_ptr(), v.data_ptr(), al.data_ptr(), be.data_ptr(),
+                                         o.data_ptr(), b_[0].data_ptr(), b_[1].data_ptr(), b_[2].data_ptr(),
+                                         b_[3].data_ptr(), B, HV, K, V, 127.0, res_fmt, 0,
+                                         _native.stream_handle(device))
+                _native.check(st, "statequant step")
+            ms = _graph_time(device, step, nsets, 3, max(2, steps // nsets))
+            rec(f"statequant_B{B}_{sq.residual_label(res_fmt)}", ms, statequant_bytes(B, HV, K, V, res_fmt))
+            del sets
+        # fp32 baseline step, ping-pong between state buffers
+        nsets = max(2, min(64, -(-(512 << 20) // (B * HV * K * V * 4))))
+        hsets = [torch.randn(B, HV, K, V, device=device, generator=gen) * 0.1 for _ in range(nsets)]
+
+        def fstep(t):
+            st = L.ck_gdn_fp32_step(hsets[t % nsets].data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                    al.data_ptr(), be.data_ptr(), o.data_ptr(), hsets[(t + 1) % nsets].data_ptr(),
+                                    B, HV, K, V, _native.stream_handle(device))
+            _native.check(st, "fp32 step")
+        ms = _graph_time(device, fstep, nsets, 3, max(2, steps // nsets))
+        rec(f"fp32_step_B{B}", ms, B * HV * (2 * 4 * K * V + 2 * 4 * K + 2 * 4 * V + 8))
+        del hsets
+        torch.cuda.empty_cache()
+    # vLLM-layout unquantized arms at B=64 (in place, slot groups rotated)
+    B = 64
+    sets_in, A_log, dt_bias = make_step_inputs(B, 4, device, 9)
+    for dtype, name, esz in ((torch.float32, "fp32", 4), (torch.bfloat16, "bf16", 2)):
+        groups = max(2, min(64, -(-(512 << 20) // (B * HV * V * K * esz))))
+        S = B * groups + 1
+        state = (torch.randn(S, HV, V, K, device=device, generator=gen) * 0.1).to(dtype)
+        idxs = [torch.arange(1 + g * B, 1 + (g + 1) * B, dtype=torch.int32, device=device) for g in range(groups)]
+        out = torch.empty(B, 1, HV, V, device=device)
+
+        def vstep(t, state=state, idxs=idxs, dtype=dtype, out=out, S=S):
+            mixed, a, b = sets_in[t % len(sets_in)]
+            st = L.ck_gdn_packed_decode_float_state(
+                mixed.data_ptr(), 0, mixed.stride(0), a.data_ptr(), 0, a.stride(0), b.data_ptr(), 0, b.stride(0),
+                A_log.data_ptr(), 0, dt_bias.data_ptr(), 0, 1.0, state.data_ptr(),
+                0 if dtype == torch.float32 else 1, state.stride(0), out.data_ptr(), 0,
+                idxs[t % len(idxs)].data_ptr(), 1, S, B, H, HV, K, V, 0, _native.stream_handle(device))
+            _native.check(st, "float-state step")
+        ms = _graph_time(device, vstep, groups, 3, max(2, steps // groups))
+        rec(f"vllm_{name}_state_B{B}", ms, float_state_bytes(B, H, HV, K, V, esz))
+        del state
+        torch.cuda.empty_cache()
+    return res
+
+
 def copy_peak(device, mib, reps):
     """Device-to-device copy of `mib` MiB (read + write), reps times."""
     n = mib * (1 << 20) // 4
@@ -332,7 +459,8 @@ def main():
                     help="time every B in {1, 8, 64, 256} x residual format x scale granularity (default: "
                          "the headline format at B in {1, 8, 64, 256} and the C2 / C4 steps)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--no-sweep", action="store_true", help="time only the headline configuration")
+    ap.add_argument("--no-sweep", action="store_true",
+                    help="time only the headline configuration (no batch sweep, no other entry points)")
     ap.add_argument("--drift", action="store_true",
                     help="instead: config C5 drift (24 layers x B=64 x 2048 tokens, int8 and int6 state) "
                          "against the fp32 state arm; prints one JSON line")
@@ -428,6 +556,8 @@ def main():
                                      "GBps": round(nb / (m * 1e-3) / 1e9, 1),
                                      "frac": round(nb / (m * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
     line["sweep"] = dict(sorted(sweep.items(), key=lambda kv: (int(kv[0][1:kv[0].index("_")]), kv[0])))
+    if not args.no_sweep:
+        line["arms"] = arms(device)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(B, resid_fmt, per_head, args.cpu_seconds)
     print(json.dumps(line), flush=True)

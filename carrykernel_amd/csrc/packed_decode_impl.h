@@ -219,40 +219,22 @@ __device__ __forceinline__ void store_resid(int8_t* dst, const uint32_t (&eb)[16
   }
 }
 
-// Compute and store one item whose registers are loaded.
-template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ESZ>
-__device__ __forceinline__ void process_item(const PackedParams& p, const ItemCoord& ic, int row0, int c, int lane,
-                                             int wave, int parity, float alpha, float beta,
-                                             const ItemRegs<RPL, Layout<K, RPL, WAVES, RESID, PER_HEAD>::EW,
-                                                            Layout<K, RPL, WAVES, RESID, PER_HEAD>::QKT>& R,
-                                             float (*s_qk)[2 * K], float (*s_red)[WAVES]) {
-  using L = Layout<K, RPL, WAVES, RESID, PER_HEAD>;
-  constexpr int LPR = L::LPR;
-  const int odt = p.out_dtype();
-  char* obase = static_cast<char*>(p.out) + ((int64_t)ic.n * p.HV + ic.hv) * p.V * (odt == kF32 ? 4 : 2);
-
-  if (!ic.live) {
-    // NULL block (slot <= 0): zeros, no state access
-    // (quantized_packed_decode.py:132-136); out-of-range ids: NaN.
-    const float fill = (ic.slot <= 0) ? 0.0f : __uint_as_float(0x7fc00000u);
-    if (c == 0) {
-#pragma unroll
-      for (int i = 0; i < RPL; ++i) {
-        const int r = row0 + i * L::RPI;
-        if (r < p.V) store_act_at(obase, (uint32_t)r, odt, fill);
-      }
-    }
-    return;
-  }
-
-  // ---- stage q, k through LDS; L2 norm and q scale once per value ----
+// Stage one item's q and k in LDS buffer `parity`: q * scale and k, both
+// L2-normalised first when the flag is set (each thread computes the norms
+// from the raw values, one division per staged value). qk holds this thread's
+// share of the raw activation bits, element threadIdx.x + j * NT of [q | k].
+// Ends with a barrier after which every thread may read the staged values.
+template <int K, int QKT, int NT, int ESZ>
+__device__ __forceinline__ void stage_qk(const PackedParams& p, const uint32_t (&qk)[QKT], int c, int parity,
+                                         float (*s_qk)[2 * K]) {
+  constexpr int LPR = K / 16;
   float* buf = s_qk[parity];
   if (p.l2norm) {
     float* raw = s_qk[2 + parity];
 #pragma unroll
-    for (int j = 0; j < L::QKT; ++j) {
-      const int e = (int)threadIdx.x + j * L::NT;
-      if (e < 2 * K) raw[e] = act_from_raw<ESZ>(R.qk[j], p.mixed_dtype());
+    for (int j = 0; j < QKT; ++j) {
+      const int e = (int)threadIdx.x + j * NT;
+      if (e < 2 * K) raw[e] = act_from_raw<ESZ>(qk[j], p.mixed_dtype());
     }
     __syncthreads();
     float sq, sk;
@@ -279,21 +261,51 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
     const float dq = sqrtf(sq + 1e-6f);
     const float dk = sqrtf(sk + 1e-6f);
 #pragma unroll
-    for (int j = 0; j < L::QKT; ++j) {
-      const int e = (int)threadIdx.x + j * L::NT;
+    for (int j = 0; j < QKT; ++j) {
+      const int e = (int)threadIdx.x + j * NT;
       if (e < 2 * K) buf[e] = (e < K) ? (raw[e] / dq) * p.scale : raw[e] / dk;
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < L::QKT; ++j) {
-      const int e = (int)threadIdx.x + j * L::NT;
+    for (int j = 0; j < QKT; ++j) {
+      const int e = (int)threadIdx.x + j * NT;
       if (e < 2 * K) {
-        const float x = act_from_raw<ESZ>(R.qk[j], p.mixed_dtype());
+        const float x = act_from_raw<ESZ>(qk[j], p.mixed_dtype());
         buf[e] = (e < K) ? x * p.scale : x;
       }
     }
   }
   __syncthreads();
+}
+
+// Compute and store one item whose registers are loaded.
+template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ESZ>
+__device__ __forceinline__ void process_item(const PackedParams& p, const ItemCoord& ic, int row0, int c, int lane,
+                                             int wave, int parity, float alpha, float beta,
+                                             const ItemRegs<RPL, Layout<K, RPL, WAVES, RESID, PER_HEAD>::EW,
+                                                            Layout<K, RPL, WAVES, RESID, PER_HEAD>::QKT>& R,
+                                             float (*s_qk)[2 * K], float (*s_red)[WAVES]) {
+  using L = Layout<K, RPL, WAVES, RESID, PER_HEAD>;
+  constexpr int LPR = L::LPR;
+  const int odt = p.out_dtype();
+  char* obase = static_cast<char*>(p.out) + ((int64_t)ic.n * p.HV + ic.hv) * p.V * (odt == kF32 ? 4 : 2);
+
+  if (!ic.live) {
+    // NULL block (slot <= 0): zeros, no state access
+    // (quantized_packed_decode.py:132-136); out-of-range ids: NaN.
+    const float fill = (ic.slot <= 0) ? 0.0f : __uint_as_float(0x7fc00000u);
+    if (c == 0) {
+#pragma unroll
+      for (int i = 0; i < RPL; ++i) {
+        const int r = row0 + i * L::RPI;
+        if (r < p.V) store_act_at(obase, (uint32_t)r, odt, fill);
+      }
+    }
+    return;
+  }
+
+  stage_qk<K, L::QKT, L::NT, ESZ>(p, R.qk, c, parity, s_qk);
+  const float* buf = s_qk[parity];
   // k and q are read from LDS for every row (not held in registers across
   // rows): 32 fewer VGPRs, so more waves per SIMD hide latency.
   const float4* q4 = reinterpret_cast<const float4*>(buf + c * 16);

@@ -31,29 +31,15 @@ constexpr int kCols = 128;   // V-columns per workgroup
 constexpr int kSlices = 8;   // K-slices per workgroup
 constexpr int kThreads = 256;
 
-// fp32 -> fp8 e5m2 with round-to-nearest-even (sign | 5-bit exponent, bias 15
-// | 2-bit mantissa; subnormals m * 2^-16; values at or past the midpoint above
-// the largest finite 57344 become inf).
-__device__ __forceinline__ uint32_t f32_to_e5m2(float f) {
-  const uint32_t u = __float_as_uint(f);
-  const uint32_t sign = (u >> 24) & 0x80u;
-  const uint32_t a = u & 0x7fffffffu;
-  if (a > 0x7f800000u) return sign | 0x7fu;
-  if (a >= 0x47700000u) return sign | 0x7cu;
-  if (a < 0x38800000u) return sign | (uint32_t)rintf(__uint_as_float(a) * 65536.0f);
-  const uint32_t lsb = (a >> 21) & 1u;
-  return sign | (((a + 0xfffffu + lsb) >> 21) - ((127u - 15u) << 2));
-}
-
-__device__ __forceinline__ float e5m2_to_f32(uint32_t b) {
-  const uint32_t sign = (b & 0x80u) << 24;
-  const uint32_t e = (b >> 2) & 0x1fu, m = b & 3u;
-  if (e == 0) {
-    const float v = (float)m * (1.0f / 65536.0f);
-    return sign ? -v : v;
-  }
-  if (e == 31) return __uint_as_float(sign | 0x7f800000u | (m << 21));
-  return __uint_as_float(sign | ((e - 15u + 127u) << 23) | (m << 21));
+// fp8 e5m2 (OCP: sign | 5-bit exponent, bias 15 | 2-bit mantissa, with
+// infinities and NaNs) through gfx950's conversion instructions: encoding
+// rounds to nearest even, keeps subnormals (m * 2^-16) and sends values at or
+// past the midpoint above the largest finite 57344 to infinity, the format's
+// own definition (the reference's torch.float8_e5m2 casts). Two values per
+// v_cvt_pk_bf8_f32 into one 16-bit half of the result; decoding picks a byte.
+__device__ __forceinline__ uint32_t f32x4_to_e5m2x4(float a, float b, float c, float d) {
+  const int lo = __builtin_amdgcn_cvt_pk_bf8_f32(a, b, 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_bf8_f32(c, d, lo, true);
 }
 
 __device__ __forceinline__ float half_bits_to_f32(uint32_t h) {
@@ -151,8 +137,10 @@ __global__ __launch_bounds__(kThreads) void quant_step_kernel(const StepParams p
         ev[r][2] = half_bits_to_f32(e2.y & 0xffffu), ev[r][3] = half_bits_to_f32(e2.y >> 16);
       } else if constexpr (RES == kResFp8) {
         const uint32_t e1 = *reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(p.e_in) + i);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) ev[r][j] = e5m2_to_f32((e1 >> (8 * j)) & 0xffu);
+        ev[r][0] = __builtin_amdgcn_cvt_f32_bf8((int)e1, 0);
+        ev[r][1] = __builtin_amdgcn_cvt_f32_bf8((int)e1, 1);
+        ev[r][2] = __builtin_amdgcn_cvt_f32_bf8((int)e1, 2);
+        ev[r][3] = __builtin_amdgcn_cvt_f32_bf8((int)e1, 3);
       } else {
         const uint32_t e1 = *reinterpret_cast<const uint32_t*>(static_cast<const int8_t*>(p.e_in) + i);
 #pragma unroll
@@ -287,8 +275,7 @@ __global__ __launch_bounds__(kThreads) void quant_step_kernel(const StepParams p
                        f32_to_half_bits(h[r][2]) | (f32_to_half_bits(h[r][3]) << 16));
       } else {
         *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(p.e_out) + i) =
-            f32_to_e5m2(h[r][0]) | (f32_to_e5m2(h[r][1]) << 8) | (f32_to_e5m2(h[r][2]) << 16) |
-            (f32_to_e5m2(h[r][3]) << 24);
+            f32x4_to_e5m2x4(h[r][0], h[r][1], h[r][2], h[r][3]);
       }
     }
   }
