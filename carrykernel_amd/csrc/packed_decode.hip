@@ -114,12 +114,9 @@ extern "C" int ck_gdn_packed_decode(const void* mixed_qkv, int qkv_dtype, int64_
   p.num_slots = (int32_t)num_slots;
   p.scale = scale;
   const int qmax = (1 << (state_bits - 1)) - 1;
-  const int qmax_e = (resid_fmt == CK_RESID_INT4) ? 7 : 127;
   volatile float one = 1.0f;  // RN(1/q) computed in fp32 on the host
   p.qmax = (float)qmax;
   p.rqmax = one / (float)qmax;
-  p.qmax_e = (float)qmax_e;
-  p.rqmax_e = one / (float)qmax_e;
   p.dtypes = qkv_dtype | (a_dtype << 4) | (b_dtype << 8) | (A_log_dtype << 12) | (dt_bias_dtype << 16) |
              (out_dtype << 20);
   p.H = H;

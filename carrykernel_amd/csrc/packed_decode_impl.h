@@ -85,7 +85,6 @@ struct PackedParams {
   int32_t num_slots;
   float scale;
   float qmax, rqmax;      // state code range and RN(1/qmax)
-  float qmax_e, rqmax_e;  // residual code range and RN(1/qmax_e)
   int32_t dtypes;         // mixed | a << 4 | b << 8 | A_log << 12 | dt_bias << 16 | out << 20
   int32_t H, HV, V;
   int32_t items;          // B * HV * nvt
@@ -102,6 +101,14 @@ struct PackedParams {
 
 constexpr int kResidInt8 = CK_RESID_INT8;
 constexpr int kResidInt4 = CK_RESID_INT4;
+
+// Residual code range qmax_e (7 for int4, 127 for int8) and RN(1 / qmax_e),
+// fixed by the residual format.
+template <int RESID>
+struct ResidRange {
+  static constexpr float q = RESID == kResidInt4 ? 7.0f : 127.0f;
+  static constexpr uint32_t rq_bits = RESID == kResidInt4 ? 0x3e124925u : 0x3c010204u;  // RN(1/7), RN(1/127)
+};
 
 template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD>
 struct Layout {
@@ -135,11 +142,12 @@ struct ItemCoord {
 // Coordinates of an item. `item` is uniform; readfirstlane keeps the results
 // in SGPRs so that the slot id is a scalar load (a vector load here would be
 // ordered behind the prefetch in the vector memory counter).
+template <bool ONE_TILE = false>  // one V-tile per (request, head): vt = 0
 __device__ __forceinline__ ItemCoord item_coord(const PackedParams& p, const int32_t* __restrict__ idx, int item) {
   ItemCoord ic;
   item = __builtin_amdgcn_readfirstlane(item);
-  const uint32_t nh = fdiv((uint32_t)item, p.div_nvt);
-  ic.vt = item - (int)(nh * p.div_nvt.d);
+  const uint32_t nh = ONE_TILE ? (uint32_t)item : fdiv((uint32_t)item, p.div_nvt);
+  ic.vt = ONE_TILE ? 0 : item - (int)(nh * p.div_nvt.d);
   const uint32_t n = fdiv(nh, p.div_hv);
   ic.hv = __builtin_amdgcn_readfirstlane((int)(nh - n * p.div_hv.d));
   ic.n = __builtin_amdgcn_readfirstlane((int)n);
@@ -411,7 +419,7 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
       eamax_local = fmaxf(eamax_local, valid ? ea : 0.0f);  // rows past V hold re-read data
     } else {
       ea = group_max<LPR>(ea);
-      const float es = fmaxf(div_small_int(ea, p.qmax_e, p.rqmax_e), kEps);
+      const float es = fmaxf(div_small_int(ea, ResidRange<RESID>::q, __uint_as_float(ResidRange<RESID>::rq_bits)), kEps);
       const float inv_e = recip_rn(es);
       uint32_t eb[16];
 #pragma unroll
@@ -431,7 +439,7 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
     float ea = s_red[parity][0];
 #pragma unroll
     for (int w = 1; w < WAVES; ++w) ea = fmaxf(ea, s_red[parity][w]);
-    const float es = fmaxf(div_small_int(ea, p.qmax_e, p.rqmax_e), kEps);
+    const float es = fmaxf(div_small_int(ea, ResidRange<RESID>::q, __uint_as_float(ResidRange<RESID>::rq_bits)), kEps);
     const float inv_e = recip_rn(es);
 #pragma unroll
     for (int i = 0; i < RPL; ++i) {
