@@ -122,6 +122,13 @@ struct Layout {
   static constexpr int RK = (RESID == kResidInt4) ? K / 2 : K;  // residual bytes per row
 };
 
+// Per-head residual mode keeps every row's unquantized residual until the
+// head's amax is known. With int8 residual rows at 2 rows per lane the 32
+// values go to LDS (each lane reads back only its own) instead of VGPRs, so
+// the 8-wave shape fits 128 VGPRs.
+template <int RPL, int RESID, bool PER_HEAD>
+constexpr bool kResidInLds = PER_HEAD && RESID == CK_RESID_INT8 && RPL == 2;
+
 // Everything one lane needs from memory for one item.
 template <int RPL, int EW, int QKT>
 struct ItemRegs {
@@ -292,8 +299,9 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
                                              int wave, int parity, float alpha, float beta,
                                              const ItemRegs<RPL, Layout<K, RPL, WAVES, RESID, PER_HEAD>::EW,
                                                             Layout<K, RPL, WAVES, RESID, PER_HEAD>::QKT>& R,
-                                             float (*s_qk)[2 * K], float (*s_red)[WAVES]) {
+                                             float (*s_qk)[2 * K], float (*s_red)[WAVES], float4* s_ek) {
   using L = Layout<K, RPL, WAVES, RESID, PER_HEAD>;
+  constexpr bool EK_LDS = kResidInLds<RPL, RESID, PER_HEAD>;
   constexpr int LPR = L::LPR;
   const int odt = p.out_dtype();
   char* obase = static_cast<char*>(p.out) + ((int64_t)ic.n * p.HV + ic.hv) * p.V * (odt == kF32 ? 4 : 2);
@@ -326,7 +334,8 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
                         : p.rscale + ic.slot * p.stride_rscale + (int64_t)ic.hv * p.V;
   const float es_head = R.es_in[0];
 
-  float ekeep[PER_HEAD ? RPL : 1][16];
+  float ekeep[PER_HEAD && !EK_LDS ? RPL : 1][16];
+  float4* ek = s_ek + (wave * RPL * 4) * 64 + lane;  // this lane's slots (EK_LDS)
   float eamax_local = 0.0f;
 
 #pragma unroll
@@ -415,7 +424,13 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
 
     if constexpr (PER_HEAD) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) ekeep[i][j] = t[j];
+      for (int j = 0; j < 16; ++j) {
+        if constexpr (EK_LDS) {
+          if ((j & 3) == 3) ek[(i * 4 + (j >> 2)) * 64] = make_float4(t[j - 3], t[j - 2], t[j - 1], t[j]);
+        } else {
+          ekeep[i][j] = t[j];
+        }
+      }
       eamax_local = fmaxf(eamax_local, valid ? ea : 0.0f);  // rows past V hold re-read data
     } else {
       ea = group_max<LPR>(ea);
@@ -446,7 +461,16 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
       const int r = row0 + i * L::RPI;
       uint32_t eb[16];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) (void)quantize<MODE>(ekeep[i][j], es, inv_e, eb[j]);
+      for (int j = 0; j < 16; ++j) {
+        float ev;
+        if constexpr (EK_LDS) {
+          const float4 e4 = ek[(i * 4 + (j >> 2)) * 64];
+          ev = (j & 3) == 0 ? e4.x : (j & 3) == 1 ? e4.y : (j & 3) == 2 ? e4.z : e4.w;
+        } else {
+          ev = ekeep[i][j];
+        }
+        (void)quantize<MODE>(ev, es, inv_e, eb[j]);
+      }
       if (r < p.V) store_resid<RESID>(ebase + (uint32_t)(r * L::RK + c * (L::RK / LPR)), eb);
     }
     if (threadIdx.x == 0) *rsb = es;
@@ -480,6 +504,7 @@ void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx)
   using L = Layout<K, RPL, WAVES, RESID, PER_HEAD>;
   __shared__ __attribute__((aligned(16))) float s_qk[4][2 * K];  // [parity] staged, [2 + parity] raw
   __shared__ float s_red[2][WAVES];
+  __shared__ float4 s_ek[kResidInLds<RPL, RESID, PER_HEAD> ? WAVES * RPL * 4 * 64 : 1];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -510,7 +535,7 @@ void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx)
       const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), k & 63));
       const float beta = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(beta_v), k & 63));
       process_item<K, RPL, WAVES, RESID, PER_HEAD, MODE, ESZ>(p, ca, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c,
-                                                          lane, wave, live & 1, alpha, beta, A, s_qk, s_red);
+                                                          lane, wave, live & 1, alpha, beta, A, s_qk, s_red, s_ek);
       live += ca.live ? 1 : 0;
     }
     if (next >= p.items) break;
@@ -526,7 +551,7 @@ void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx)
       const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), k & 63));
       const float beta = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(beta_v), k & 63));
       process_item<K, RPL, WAVES, RESID, PER_HEAD, MODE, ESZ>(p, cb, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c,
-                                                          lane, wave, live & 1, alpha, beta, B, s_qk, s_red);
+                                                          lane, wave, live & 1, alpha, beta, B, s_qk, s_red, s_ek);
       live += cb.live ? 1 : 0;
     }
     if (next >= p.items) break;
@@ -576,7 +601,7 @@ int launch_k(const PackedParams& p, int B, hipStream_t stream) {
     return launch_cfg<K, 4, 1, RESID, false, MODE, ESZ>(p, B, stream);
   } else {
     const int need = p.V;
-    if constexpr (K == 128 && RESID == kResidInt4) {
+    if constexpr (K == 128) {
       if (need > RPI * 4 * 2 && need <= RPI * 2 * 8) return launch_cfg<K, 2, 8, RESID, true, MODE, ESZ>(p, B, stream);
     }
     if (need <= RPI * 4 * 1) return launch_cfg<K, 4, 1, RESID, true, MODE, ESZ>(p, B, stream);
