@@ -588,10 +588,10 @@ int launch_cfg(PackedParams p, int B, hipStream_t stream) {
 // instruction covers 8 rows). With per-row residual scales a workgroup is 4
 // waves of 2 rows per lane (64-row tiles, four workgroups per CU) when that
 // gives 512 tiles or more, else 1 wave of 4 rows per lane (32-row tiles). A
-// per-head residual scale needs the whole head in one workgroup; with the
-// packed int4 residual at K=128 that is 8 waves of 2 rows per lane, which fits
-// 128 VGPRs and so two workgroups per CU (int8 residual rows need more
-// registers and keep 4 rows per lane).
+// per-head residual scale needs the whole head in one workgroup; at K=128 that
+// is 8 waves of 2 rows per lane, which fits 128 VGPRs (the int8 residual's
+// unquantized values wait for the head amax in LDS) and so two workgroups per
+// CU; other K keep 4 rows per lane.
 template <int K, int RESID, bool PER_HEAD, int MODE, int ESZ>
 int launch_k(const PackedParams& p, int B, hipStream_t stream) {
   constexpr int RPI = 64 / (K / 16);
