@@ -224,7 +224,8 @@ def run_config(device, B, resid_fmt, per_head, steps, warmup, groups, quant_mode
 
 def _graph_time(device, step, n_steps, warmup, reps_cap=None):
     """Device ms per step of `step(t)` captured as n_steps consecutive launches
-    in one HIP graph and replayed (warm-up replays first)."""
+    in one HIP graph and replayed (warm-up replays first; median of three
+    timed batches)."""
     side = torch.cuda.Stream(device)
     side.wait_stream(torch.cuda.current_stream(device))
     with torch.cuda.stream(side):
@@ -241,13 +242,15 @@ def _graph_time(device, step, n_steps, warmup, reps_cap=None):
         graph.replay()
     torch.cuda.synchronize()
     reps = reps_cap or 20
-    timer = Timer(device)
-    timer.start()
-    for _ in range(reps):
-        graph.replay()
-    ms = timer.stop_ms() / (reps * n_steps)
+    trials = []
+    for _ in range(3):   # median of three timed batches of replays
+        timer = Timer(device)
+        timer.start()
+        for _ in range(reps):
+            graph.replay()
+        trials.append(timer.stop_ms() / (reps * n_steps))
     del graph
-    return ms
+    return sorted(trials)[1]
 
 
 def statequant_bytes(B, HV, K, V, res_fmt):
