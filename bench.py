@@ -163,9 +163,11 @@ class Timer:
         return self.s.elapsed_time(self.e)
 
 
-def run_config(device, B, resid_fmt, per_head, steps, warmup, groups, quant_mode="fast", seed=0):
+def run_config(device, B, resid_fmt, per_head, steps, warmup, groups, quant_mode="fast", seed=0,
+               act_dtype=torch.float32):
     """Returns (device ms per step from a replayed graph, host-inclusive ms per
-    eager call). The graph holds one step per slot group."""
+    eager call). The graph holds one step per slot group. `act_dtype` is the
+    dtype of mixed_qkv, a, b and out (vLLM runs bf16 activations)."""
     S = B * groups + 1
     state = warm_state(S, device, seed)
     pool = qpd.init_quantized_state(S, HV, V, K, device, h0=state, resid_fmt=resid_fmt,
@@ -173,9 +175,10 @@ def run_config(device, B, resid_fmt, per_head, steps, warmup, groups, quant_mode
     del state
     torch.cuda.empty_cache()
     sets, A_log, dt_bias = make_step_inputs(B, 8, device, seed + 1)
+    sets = [tuple(x.to(act_dtype) for x in st) for st in sets]
     perm = torch.randperm(S - 1, generator=torch.Generator().manual_seed(seed)) + 1
     idx_groups = [perm[i * B:(i + 1) * B].to(torch.int32).to(device) for i in range(groups)]
-    out = torch.empty(B, 1, HV, V, device=device)
+    out = torch.empty(B, 1, HV, V, device=device, dtype=act_dtype)
 
     def step(t):
         mixed, a, b = sets[t % len(sets)]
@@ -558,6 +561,13 @@ def main():
         sweep[f"B{bb}_{fmt_name}"] = {"us": round(m * 1e3, 3), "host_us": round(hm * 1e3, 3),
                                      "GBps": round(nb / (m * 1e-3) / 1e9, 1),
                                      "frac": round(nb / (m * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+    if not args.no_sweep:   # the headline step with vLLM's bf16 activations and output
+        m, hm = run_config(device, 64, qpd.RESID_INT4, True, max(200, args.steps // 4), 50, 16, args.quant_mode,
+                           act_dtype=torch.bfloat16)
+        nb = algorithmic_bytes(64, H, HV, K, V, qpd.RESID_INT4, True, act_bytes=2)
+        sweep["B64_int4_head_bf16act"] = {"us": round(m * 1e3, 3), "host_us": round(hm * 1e3, 3),
+                                          "GBps": round(nb / (m * 1e-3) / 1e9, 1),
+                                          "frac": round(nb / (m * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
     line["sweep"] = dict(sorted(sweep.items(), key=lambda kv: (int(kv[0][1:kv[0].index("_")]), kv[0])))
     if not args.no_sweep:
         line["arms"] = arms(device)

@@ -38,7 +38,7 @@ __device__ __forceinline__ float load_act(const void* p, int64_t i, int dtype) {
 
 // Raw bits of one activation of ESZ bytes (4: fp32, 2: bf16 / fp16) at a
 // uniform base plus a 32-bit byte offset. Conversion is deferred to
-// act_from_raw so that issuing the load never waits for its data.
+// act_decode so that issuing the load never waits for its data.
 template <int ESZ>
 __device__ __forceinline__ uint32_t load_act_raw(const char* base, uint32_t off) {
   if constexpr (ESZ == 4) {
@@ -48,15 +48,23 @@ __device__ __forceinline__ uint32_t load_act_raw(const char* base, uint32_t off)
   }
 }
 
-template <int ESZ>
-__device__ __forceinline__ float act_from_raw(uint32_t raw, int dtype) {
-  if constexpr (ESZ == 4) return __uint_as_float(raw);  // 4-byte activations are fp32
-  if (dtype == kF32) return __uint_as_float(raw);
-  if (dtype == kBF16) return __uint_as_float(raw << 16);
-  _Float16 h;
-  const uint16_t r16 = (uint16_t)raw;
-  __builtin_memcpy(&h, &r16, 2);
-  return (float)h;
+// Bytes of one activation of dtype ACT, and its decode from raw bits with the
+// dtype fixed at compile time.
+template <int ACT>
+constexpr int act_bytes = ACT == kF32 ? 4 : 2;
+
+template <int ACT>
+__device__ __forceinline__ float act_decode(uint32_t raw) {
+  if constexpr (ACT == kF32) {
+    return __uint_as_float(raw);
+  } else if constexpr (ACT == kBF16) {
+    return __uint_as_float(raw << 16);
+  } else {
+    _Float16 h;
+    const uint16_t r16 = (uint16_t)raw;
+    __builtin_memcpy(&h, &r16, 2);
+    return (float)h;
+  }
 }
 
 // Access at a uniform base plus a 32-bit byte offset (lets the compiler use

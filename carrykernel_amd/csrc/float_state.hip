@@ -40,11 +40,12 @@ using FLayout = pd::Layout<K, RPL, WAVES, pd::kResidInt8, false>;
 
 // All loads of one item, branch-free (see pd::load_item): an unneeded item
 // collapses onto the first bytes of slot 0; rows past V re-read row V-1.
-template <int K, int RPL, int WAVES, bool BF16, int ESZ>
+template <int K, int RPL, int WAVES, bool BF16, int ACT>
 __device__ __forceinline__ void load_fitem(const PackedParams& p, const ItemCoord& ic, bool needed, int row0, int c,
                                            FloatItemRegs<RPL, FLayout<K, RPL, WAVES>::QKT, BF16>& R) {
   using L = FLayout<K, RPL, WAVES>;
   constexpr uint32_t SB = BF16 ? 2u : 4u;  // state bytes per element
+  constexpr int ESZ = act_bytes<ACT>;
   const bool real = needed && ic.live;
   const uint32_t keep = real ? 0xffffffffu : 0u;
   const int64_t slot = real ? ic.slot : 0;
@@ -74,7 +75,7 @@ __device__ __forceinline__ void load_fitem(const PackedParams& p, const ItemCoor
   }
 }
 
-template <int K, int RPL, int WAVES, bool BF16, int ESZ>
+template <int K, int RPL, int WAVES, bool BF16, int ACT>
 __device__ __forceinline__ void process_fitem(const PackedParams& p, const ItemCoord& ic, int row0, int c,
                                               int parity, float alpha, float beta,
                                               const FloatItemRegs<RPL, FLayout<K, RPL, WAVES>::QKT, BF16>& R,
@@ -96,7 +97,7 @@ __device__ __forceinline__ void process_fitem(const PackedParams& p, const ItemC
     }
     return;
   }
-  pd::stage_qk<K, L::QKT, L::NT, ESZ>(p, R.qk, c, parity, s_qk);
+  pd::stage_qk<K, L::QKT, L::NT, ACT>(p, R.qk, c, parity, s_qk);
   const float* buf = s_qk[parity];
   const float4* q4 = reinterpret_cast<const float4*>(buf + c * 16);
   const float4* k4 = reinterpret_cast<const float4*>(buf + K + c * 16);
@@ -128,7 +129,7 @@ __device__ __forceinline__ void process_fitem(const PackedParams& p, const ItemC
 #pragma unroll
     for (int j = 1; j < 16; ++j) rd = fmaf(h[j], kk[j], rd);
     rd = group_sum<LPR>(rd);
-    const float dv = beta * (act_from_raw<ESZ>(R.vv[i], p.mixed_dtype()) - rd);
+    const float dv = beta * (act_decode<ACT>(R.vv[i]) - rd);
 #pragma unroll
     for (int j = 0; j < 16; ++j) h[j] = fmaf(kk[j], dv, h[j]);
 #pragma unroll
@@ -165,7 +166,7 @@ __device__ __forceinline__ void process_fitem(const PackedParams& p, const ItemC
   }
 }
 
-template <int K, int RPL, int WAVES, bool BF16, int ESZ>
+template <int K, int RPL, int WAVES, bool BF16, int ACT>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
 void float_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx) {
   using L = FLayout<K, RPL, WAVES>;
@@ -182,15 +183,15 @@ void float_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx) 
   // packed_decode_kernel)
   FloatItemRegs<RPL, L::QKT, BF16> A, B;
   ItemCoord ca = pd::item_coord(p, idx, item), cb;
-  load_fitem<K, RPL, WAVES, BF16, ESZ>(p, ca, true, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, A);
+  load_fitem<K, RPL, WAVES, BF16, ACT>(p, ca, true, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, A);
   float alpha_v, beta_v;
   pd::gates_for_items(p, 0, lane, alpha_v, beta_v);
   int k = 0, live = 0;
   for (;;) {
     int next = item + stride;
     cb = pd::item_coord(p, idx, min(next, last));
-    load_fitem<K, RPL, WAVES, BF16, ESZ>(p, cb, next < p.items, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, B);
-    process_fitem<K, RPL, WAVES, BF16, ESZ>(p, ca, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, live & 1,
+    load_fitem<K, RPL, WAVES, BF16, ACT>(p, cb, next < p.items, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, B);
+    process_fitem<K, RPL, WAVES, BF16, ACT>(p, ca, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, live & 1,
                                             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), k & 63)),
                                             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(beta_v), k & 63)),
                                             A, s_qk);
@@ -202,8 +203,8 @@ void float_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx) 
 
     next = item + stride;
     ca = pd::item_coord(p, idx, min(next, last));
-    load_fitem<K, RPL, WAVES, BF16, ESZ>(p, ca, next < p.items, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, A);
-    process_fitem<K, RPL, WAVES, BF16, ESZ>(p, cb, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, live & 1,
+    load_fitem<K, RPL, WAVES, BF16, ACT>(p, ca, next < p.items, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, A);
+    process_fitem<K, RPL, WAVES, BF16, ACT>(p, cb, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, live & 1,
                                             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), k & 63)),
                                             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(beta_v), k & 63)),
                                             B, s_qk);
@@ -215,7 +216,7 @@ void float_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx) 
   }
 }
 
-template <int K, bool BF16, int ESZ>
+template <int K, bool BF16, int ACT>
 int launch_fs(PackedParams p, int B, hipStream_t stream) {
   constexpr int RPL = 2, WAVES = 4;
   using L = FLayout<K, RPL, WAVES>;
@@ -226,7 +227,7 @@ int launch_fs(PackedParams p, int B, hipStream_t stream) {
   p.items = (int)items;
   p.div_nvt = pd::make_fastdiv((uint32_t)nvt);
   p.div_hv = pd::make_fastdiv((uint32_t)p.HV);
-  auto fn = float_decode_kernel<K, RPL, WAVES, BF16, ESZ>;
+  auto fn = float_decode_kernel<K, RPL, WAVES, BF16, ACT>;
   const int resident = pd::resident_workgroups(reinterpret_cast<const void*>(fn), WAVES * 64);
   if (resident <= 0) return fail(CK_ELAUNCH, "cannot query the device occupancy");
   const int per_wg = (p.items + resident - 1) / resident;
@@ -235,14 +236,14 @@ int launch_fs(PackedParams p, int B, hipStream_t stream) {
   return check_launch("ck_gdn_packed_decode_float_state");
 }
 
-template <bool BF16, int ESZ>
+template <bool BF16, int ACT>
 int launch_fs_k(const PackedParams& p, int B, int K, hipStream_t s) {
   switch (K) {
-    case 16: return launch_fs<16, BF16, ESZ>(p, B, s);
-    case 32: return launch_fs<32, BF16, ESZ>(p, B, s);
-    case 64: return launch_fs<64, BF16, ESZ>(p, B, s);
-    case 128: return launch_fs<128, BF16, ESZ>(p, B, s);
-    case 256: return launch_fs<256, BF16, ESZ>(p, B, s);
+    case 16: return launch_fs<16, BF16, ACT>(p, B, s);
+    case 32: return launch_fs<32, BF16, ACT>(p, B, s);
+    case 64: return launch_fs<64, BF16, ACT>(p, B, s);
+    case 128: return launch_fs<128, BF16, ACT>(p, B, s);
+    case 256: return launch_fs<256, BF16, ACT>(p, B, s);
     default: return fail(CK_EUNSUPPORTED, "K must be one of 16, 32, 64, 128, 256, got %d", K);
   }
 }
@@ -313,6 +314,8 @@ extern "C" int ck_gdn_packed_decode_float_state(const void* mixed_qkv, int qkv_d
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool bf16 = state_dtype == CK_DTYPE_BF16;
   if (qkv_dtype == CK_DTYPE_F32)
-    return bf16 ? fs::launch_fs_k<true, 4>(p, B, K, s) : fs::launch_fs_k<false, 4>(p, B, K, s);
-  return bf16 ? fs::launch_fs_k<true, 2>(p, B, K, s) : fs::launch_fs_k<false, 2>(p, B, K, s);
+    return bf16 ? fs::launch_fs_k<true, kF32>(p, B, K, s) : fs::launch_fs_k<false, kF32>(p, B, K, s);
+  if (qkv_dtype == CK_DTYPE_BF16)
+    return bf16 ? fs::launch_fs_k<true, kBF16>(p, B, K, s) : fs::launch_fs_k<false, kBF16>(p, B, K, s);
+  return bf16 ? fs::launch_fs_k<true, kF16>(p, B, K, s) : fs::launch_fs_k<false, kF16>(p, B, K, s);
 }

@@ -126,13 +126,12 @@ extern "C" int ck_gdn_packed_decode(const void* mixed_qkv, int qkv_dtype, int64_
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int per_head = rscale_mode == CK_RSCALE_PER_HEAD;
   const int mode = quant_mode == CK_QUANT_EXACT ? kExact : kFast;
-  const int esz = qkv_dtype == CK_DTYPE_F32 ? 4 : 2;
   switch (K) {
-    case 16: return launch_for_k<16>(p, B, resid_fmt, per_head, mode, esz, s);
-    case 32: return launch_for_k<32>(p, B, resid_fmt, per_head, mode, esz, s);
-    case 64: return launch_for_k<64>(p, B, resid_fmt, per_head, mode, esz, s);
-    case 128: return launch_for_k<128>(p, B, resid_fmt, per_head, mode, esz, s);
-    default: return launch_for_k<256>(p, B, resid_fmt, per_head, mode, esz, s);
+    case 16: return launch_for_k<16>(p, B, resid_fmt, per_head, mode, qkv_dtype, s);
+    case 32: return launch_for_k<32>(p, B, resid_fmt, per_head, mode, qkv_dtype, s);
+    case 64: return launch_for_k<64>(p, B, resid_fmt, per_head, mode, qkv_dtype, s);
+    case 128: return launch_for_k<128>(p, B, resid_fmt, per_head, mode, qkv_dtype, s);
+    default: return launch_for_k<256>(p, B, resid_fmt, per_head, mode, qkv_dtype, s);
   }
 }
 

@@ -171,11 +171,12 @@ __device__ __forceinline__ ItemCoord item_coord(const PackedParams& p, const int
 // lane onto the first bytes of slot 0 / head 0, one cache line per load, and
 // its values are never used. Rows past V re-read row V-1. Bases are uniform;
 // per-lane offsets are 32-bit.
-template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int ESZ>
+template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int ACT>
 __device__ __forceinline__ void load_item(const PackedParams& p, const ItemCoord& ic, bool needed, int row0, int c,
                                           ItemRegs<RPL, Layout<K, RPL, WAVES, RESID, PER_HEAD>::EW,
                                                    Layout<K, RPL, WAVES, RESID, PER_HEAD>::QKT>& R) {
   using L = Layout<K, RPL, WAVES, RESID, PER_HEAD>;
+  constexpr int ESZ = act_bytes<ACT>;
   const bool real = needed && ic.live;
   const uint32_t keep = real ? 0xffffffffu : 0u;  // per-lane offset mask
   const int64_t slot = real ? ic.slot : 0;
@@ -239,7 +240,7 @@ __device__ __forceinline__ void store_resid(int8_t* dst, const uint32_t (&eb)[16
 // from the raw values, one division per staged value). qk holds this thread's
 // share of the raw activation bits, element threadIdx.x + j * NT of [q | k].
 // Ends with a barrier after which every thread may read the staged values.
-template <int K, int QKT, int NT, int ESZ>
+template <int K, int QKT, int NT, int ACT>
 __device__ __forceinline__ void stage_qk(const PackedParams& p, const uint32_t (&qk)[QKT], int c, int parity,
                                          float (*s_qk)[2 * K]) {
   constexpr int LPR = K / 16;
@@ -249,7 +250,7 @@ __device__ __forceinline__ void stage_qk(const PackedParams& p, const uint32_t (
 #pragma unroll
     for (int j = 0; j < QKT; ++j) {
       const int e = (int)threadIdx.x + j * NT;
-      if (e < 2 * K) raw[e] = act_from_raw<ESZ>(qk[j], p.mixed_dtype());
+      if (e < 2 * K) raw[e] = act_decode<ACT>(qk[j]);
     }
     __syncthreads();
     float sq, sk;
@@ -285,7 +286,7 @@ __device__ __forceinline__ void stage_qk(const PackedParams& p, const uint32_t (
     for (int j = 0; j < QKT; ++j) {
       const int e = (int)threadIdx.x + j * NT;
       if (e < 2 * K) {
-        const float x = act_from_raw<ESZ>(qk[j], p.mixed_dtype());
+        const float x = act_decode<ACT>(qk[j]);
         buf[e] = (e < K) ? x * p.scale : x;
       }
     }
@@ -294,7 +295,7 @@ __device__ __forceinline__ void stage_qk(const PackedParams& p, const uint32_t (
 }
 
 // Compute and store one item whose registers are loaded.
-template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ESZ>
+template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ACT>
 __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCoord& ic, int row0, int c, int lane,
                                              int wave, int parity, float alpha, float beta,
                                              const ItemRegs<RPL, Layout<K, RPL, WAVES, RESID, PER_HEAD>::EW,
@@ -320,7 +321,7 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
     return;
   }
 
-  stage_qk<K, L::QKT, L::NT, ESZ>(p, R.qk, c, parity, s_qk);
+  stage_qk<K, L::QKT, L::NT, ACT>(p, R.qk, c, parity, s_qk);
   const float* buf = s_qk[parity];
   // k and q are read from LDS for every row (not held in registers across
   // rows): 32 fewer VGPRs, so more waves per SIMD hide latency.
@@ -367,7 +368,7 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
 #pragma unroll
     for (int j = 1; j < 16; ++j) rd = fmaf(h[j], kk[j], rd);
     rd = group_sum<LPR>(rd);
-    const float dv = beta * (act_from_raw<ESZ>(R.vv[i], p.mixed_dtype()) - rd);
+    const float dv = beta * (act_decode<ACT>(R.vv[i]) - rd);
 #pragma unroll
     for (int j = 0; j < 16; ++j) h[j] = madd<MODE>(kk[j], dv, h[j]);
 #pragma unroll
@@ -498,7 +499,7 @@ __device__ __forceinline__ void gates_for_items(const PackedParams& p, int kbase
 template <int RPL, int WAVES>
 constexpr int kMinWavesPerEU = (RPL == 2 && (WAVES == 8 || WAVES == 4)) ? 4 : 1;
 
-template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ESZ>
+template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ACT>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(kMinWavesPerEU<RPL, WAVES>)))
 void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx) {
   using L = Layout<K, RPL, WAVES, RESID, PER_HEAD>;
@@ -521,7 +522,7 @@ void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx)
   // one buffer are always separated by the barrier of the live item between.
   ItemRegs<RPL, L::EW, L::QKT> A, B;
   ItemCoord ca = item_coord(p, idx, item), cb;
-  load_item<K, RPL, WAVES, RESID, PER_HEAD, ESZ>(p, ca, true, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, A);
+  load_item<K, RPL, WAVES, RESID, PER_HEAD, ACT>(p, ca, true, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, A);
   float alpha_v, beta_v;
   gates_for_items(p, 0, lane, alpha_v, beta_v);  // its loads overlap the first item's
   int k = 0;     // item number within this workgroup
@@ -530,11 +531,11 @@ void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx)
     // ---- item k in A; prefetch item k+1 into B (past the end: re-read the last item) ----
     int next = item + stride;
     cb = item_coord(p, idx, min(next, last));
-    load_item<K, RPL, WAVES, RESID, PER_HEAD, ESZ>(p, cb, next < p.items, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, B);
+    load_item<K, RPL, WAVES, RESID, PER_HEAD, ACT>(p, cb, next < p.items, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, B);
     {
       const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), k & 63));
       const float beta = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(beta_v), k & 63));
-      process_item<K, RPL, WAVES, RESID, PER_HEAD, MODE, ESZ>(p, ca, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c,
+      process_item<K, RPL, WAVES, RESID, PER_HEAD, MODE, ACT>(p, ca, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c,
                                                           lane, wave, live & 1, alpha, beta, A, s_qk, s_red, s_ek);
       live += ca.live ? 1 : 0;
     }
@@ -546,11 +547,11 @@ void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx)
     // ---- item k in B; prefetch item k+1 into A ----
     next = item + stride;
     ca = item_coord(p, idx, min(next, last));
-    load_item<K, RPL, WAVES, RESID, PER_HEAD, ESZ>(p, ca, next < p.items, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, A);
+    load_item<K, RPL, WAVES, RESID, PER_HEAD, ACT>(p, ca, next < p.items, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, A);
     {
       const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), k & 63));
       const float beta = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(beta_v), k & 63));
-      process_item<K, RPL, WAVES, RESID, PER_HEAD, MODE, ESZ>(p, cb, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c,
+      process_item<K, RPL, WAVES, RESID, PER_HEAD, MODE, ACT>(p, cb, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c,
                                                           lane, wave, live & 1, alpha, beta, B, s_qk, s_red, s_ek);
       live += cb.live ? 1 : 0;
     }
@@ -564,7 +565,7 @@ void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx)
 // Resident workgroups per GPU for a kernel (occupancy x CUs), cached per device.
 int resident_workgroups(const void* fn, int block);
 
-template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ESZ>
+template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ACT>
 int launch_cfg(PackedParams p, int B, hipStream_t stream) {
   using L = Layout<K, RPL, WAVES, RESID, PER_HEAD>;
   const int nvt = PER_HEAD ? 1 : (p.V + L::ROWS_WG - 1) / L::ROWS_WG;
@@ -574,7 +575,7 @@ int launch_cfg(PackedParams p, int B, hipStream_t stream) {
   p.items = (int)items;
   p.div_nvt = make_fastdiv((uint32_t)nvt);
   p.div_hv = make_fastdiv((uint32_t)p.HV);
-  auto fn = packed_decode_kernel<K, RPL, WAVES, RESID, PER_HEAD, MODE, ESZ>;
+  auto fn = packed_decode_kernel<K, RPL, WAVES, RESID, PER_HEAD, MODE, ACT>;
   const int resident = resident_workgroups(reinterpret_cast<const void*>(fn), WAVES * 64);
   if (resident <= 0) return fail(CK_ELAUNCH, "cannot query the device occupancy");
   // fewest items per workgroup, then the fewest workgroups achieving it
@@ -592,56 +593,52 @@ int launch_cfg(PackedParams p, int B, hipStream_t stream) {
 // is 8 waves of 2 rows per lane, which fits 128 VGPRs (the int8 residual's
 // unquantized values wait for the head amax in LDS) and so two workgroups per
 // CU; other K keep 4 rows per lane.
-template <int K, int RESID, bool PER_HEAD, int MODE, int ESZ>
+template <int K, int RESID, bool PER_HEAD, int MODE, int ACT>
 int launch_k(const PackedParams& p, int B, hipStream_t stream) {
   constexpr int RPI = 64 / (K / 16);
   if constexpr (!PER_HEAD) {
     if ((int64_t)B * p.HV * ((p.V + RPI * 8 - 1) / (RPI * 8)) >= 512)
-      return launch_cfg<K, 2, 4, RESID, false, MODE, ESZ>(p, B, stream);
-    return launch_cfg<K, 4, 1, RESID, false, MODE, ESZ>(p, B, stream);
+      return launch_cfg<K, 2, 4, RESID, false, MODE, ACT>(p, B, stream);
+    return launch_cfg<K, 4, 1, RESID, false, MODE, ACT>(p, B, stream);
   } else {
     const int need = p.V;
     if constexpr (K == 128) {
-      if (need > RPI * 4 * 2 && need <= RPI * 2 * 8) return launch_cfg<K, 2, 8, RESID, true, MODE, ESZ>(p, B, stream);
+      if (need > RPI * 4 * 2 && need <= RPI * 2 * 8) return launch_cfg<K, 2, 8, RESID, true, MODE, ACT>(p, B, stream);
     }
-    if (need <= RPI * 4 * 1) return launch_cfg<K, 4, 1, RESID, true, MODE, ESZ>(p, B, stream);
-    if (need <= RPI * 4 * 2) return launch_cfg<K, 4, 2, RESID, true, MODE, ESZ>(p, B, stream);
-    if (need <= RPI * 4 * 4) return launch_cfg<K, 4, 4, RESID, true, MODE, ESZ>(p, B, stream);
-    if (need <= RPI * 4 * 8) return launch_cfg<K, 4, 8, RESID, true, MODE, ESZ>(p, B, stream);
+    if (need <= RPI * 4 * 1) return launch_cfg<K, 4, 1, RESID, true, MODE, ACT>(p, B, stream);
+    if (need <= RPI * 4 * 2) return launch_cfg<K, 4, 2, RESID, true, MODE, ACT>(p, B, stream);
+    if (need <= RPI * 4 * 4) return launch_cfg<K, 4, 4, RESID, true, MODE, ACT>(p, B, stream);
+    if (need <= RPI * 4 * 8) return launch_cfg<K, 4, 8, RESID, true, MODE, ACT>(p, B, stream);
     return fail(CK_EUNSUPPORTED, "per-head residual scale supports V <= %d at K=%d, got V=%d", RPI * 32, K, p.V);
   }
 }
 
-// Dispatch over residual format, scale granularity, mode and activation size
-// for one K (defined in packed_decode_k<K>.hip).
-template <int K>
-int launch_for_k(const PackedParams& p, int B, int resid_fmt, int per_head, int mode, int esz, hipStream_t stream);
+// Dispatch over residual format, scale granularity, mode and activation dtype
+// for one K (launch_for_k is defined in packed_decode_k<K>.hip).
+template <int K, int ACT>
+int launch_for_act(const PackedParams& p, int B, int resid_fmt, int per_head, int mode, hipStream_t s) {
+  const bool i4 = resid_fmt == CK_RESID_INT4;
+  if (mode == kFast)
+    return i4 ? (per_head ? launch_k<K, kResidInt4, true, kFast, ACT>(p, B, s)
+                          : launch_k<K, kResidInt4, false, kFast, ACT>(p, B, s))
+              : (per_head ? launch_k<K, kResidInt8, true, kFast, ACT>(p, B, s)
+                          : launch_k<K, kResidInt8, false, kFast, ACT>(p, B, s));
+  return i4 ? (per_head ? launch_k<K, kResidInt4, true, kExact, ACT>(p, B, s)
+                        : launch_k<K, kResidInt4, false, kExact, ACT>(p, B, s))
+            : (per_head ? launch_k<K, kResidInt8, true, kExact, ACT>(p, B, s)
+                        : launch_k<K, kResidInt8, false, kExact, ACT>(p, B, s));
+}
 
-#define CK_PD_DEFINE_LAUNCH_FOR_K(KV)                                                                         \
-  template <>                                                                                                 \
-  int launch_for_k<KV>(const PackedParams& p, int B, int resid_fmt, int per_head, int mode, int esz,          \
-                       hipStream_t s) {                                                                       \
-    const bool i4 = resid_fmt == CK_RESID_INT4;                                                               \
-    if (esz == 4) {                                                                                           \
-      if (mode == kFast)                                                                                      \
-        return i4 ? (per_head ? launch_k<KV, kResidInt4, true, kFast, 4>(p, B, s)                                \
-                              : launch_k<KV, kResidInt4, false, kFast, 4>(p, B, s))                              \
-                  : (per_head ? launch_k<KV, kResidInt8, true, kFast, 4>(p, B, s)                                \
-                              : launch_k<KV, kResidInt8, false, kFast, 4>(p, B, s));                             \
-      return i4 ? (per_head ? launch_k<KV, kResidInt4, true, kExact, 4>(p, B, s)                                 \
-                            : launch_k<KV, kResidInt4, false, kExact, 4>(p, B, s))                               \
-                : (per_head ? launch_k<KV, kResidInt8, true, kExact, 4>(p, B, s)                                 \
-                            : launch_k<KV, kResidInt8, false, kExact, 4>(p, B, s));                              \
-    }                                                                                                         \
-    if (mode == kFast)                                                                                        \
-      return i4 ? (per_head ? launch_k<KV, kResidInt4, true, kFast, 2>(p, B, s)                                  \
-                            : launch_k<KV, kResidInt4, false, kFast, 2>(p, B, s))                                \
-                : (per_head ? launch_k<KV, kResidInt8, true, kFast, 2>(p, B, s)                                  \
-                            : launch_k<KV, kResidInt8, false, kFast, 2>(p, B, s));                               \
-    return i4 ? (per_head ? launch_k<KV, kResidInt4, true, kExact, 2>(p, B, s)                                   \
-                          : launch_k<KV, kResidInt4, false, kExact, 2>(p, B, s))                                 \
-              : (per_head ? launch_k<KV, kResidInt8, true, kExact, 2>(p, B, s)                                   \
-                          : launch_k<KV, kResidInt8, false, kExact, 2>(p, B, s));                                \
+template <int K>
+int launch_for_k(const PackedParams& p, int B, int resid_fmt, int per_head, int mode, int act, hipStream_t stream);
+
+#define CK_PD_DEFINE_LAUNCH_FOR_K(KV)                                                                     \
+  template <>                                                                                             \
+  int launch_for_k<KV>(const PackedParams& p, int B, int resid_fmt, int per_head, int mode, int act,      \
+                       hipStream_t s) {                                                                   \
+    if (act == kF32) return launch_for_act<KV, kF32>(p, B, resid_fmt, per_head, mode, s);                 \
+    if (act == kBF16) return launch_for_act<KV, kBF16>(p, B, resid_fmt, per_head, mode, s);               \
+    return launch_for_act<KV, kF16>(p, B, resid_fmt, per_head, mode, s);                                  \
   }
 
 }  // namespace pd
