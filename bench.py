@@ -367,6 +367,34 @@ def copy_peak(device, mib, reps):
             "GBps": round(moved / (ms * 1e-3) / 1e9, 1)}
 
 
+def hbm_copy_peak(device, total_bytes, pool_bytes=1 << 31, grids=(512, 2048, 4096)):
+    """Measured HBM ceiling beside the spec-sheet one: the library's streaming
+    copy (ck_hbm_copy) moving `total_bytes` per launch (half read, half
+    written), timed like the decode (graph-replayed, rotating over buffer
+    pairs that together exceed the 256 MB MALL); best of a few grid sizes."""
+    from carrykernel_amd import _native
+    L = _native.lib()
+    half = (total_bytes // 2) // 4096 * 4096
+    groups = int(max(2, min(64, pool_bytes // (2 * half))))
+    src = [torch.empty(half, dtype=torch.uint8, device=device).fill_(t + 1) for t in range(groups)]
+    dst = [torch.empty(half, dtype=torch.uint8, device=device) for _ in range(groups)]
+    best = None
+    for grid in grids:
+        def step(t, grid=grid):
+            _native.check(L.ck_hbm_copy(src[t % groups].data_ptr(), dst[t % groups].data_ptr(), half, grid,
+                                        _native.stream_handle(device)), "hbm copy")
+        ms = _graph_time(device, step, groups, 3)
+        if best is None or ms < best[0]:
+            best = (ms, grid)
+    if not all(bool((d[:4096] == t + 1).all()) for t, d in enumerate(dst)):
+        raise RuntimeError("hbm copy produced wrong bytes")
+    del src, dst
+    torch.cuda.empty_cache()
+    ms, grid = best
+    return {"bytes_per_launch": 2 * half, "us": round(ms * 1e3, 3), "GBps": round(2 * half / (ms * 1e-3) / 1e9, 1),
+            "grid": grid}
+
+
 def float_state_step(state, mixed, a, b, A_log, dt_bias, scale, out, idx, l2norm):
     """One step of the unquantized fp32 state arm (ck_gdn_packed_decode_float_state)."""
     from carrykernel_amd import _native
@@ -571,6 +599,13 @@ def main():
     line["sweep"] = dict(sorted(sweep.items(), key=lambda kv: (int(kv[0][1:kv[0].index("_")]), kv[0])))
     if not args.no_sweep:
         line["arms"] = arms(device)
+        # measured copy ceiling at the headline's byte count and for a 1 GiB copy
+        at = hbm_copy_peak(device, nbytes)
+        big = hbm_copy_peak(device, 1 << 30)
+        line["copy_peak"] = {"kernel": "ck_hbm_copy (16 B non-temporal load + store per lane, grid-stride)",
+                             "at_workload_bytes": at, "large": big,
+                             "frac_of_copy_at_workload": round(gbps / at["GBps"], 4),
+                             "frac_of_copy_large": round(gbps / big["GBps"], 4)}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(B, resid_fmt, per_head, args.cpu_seconds)
     print(json.dumps(line), flush=True)

@@ -80,6 +80,7 @@ _SIGNATURES = {
         _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _vp]),
     "ck_quantize_rows": (_int, [_vp, _int, _i64, _i64, _int, _flt, _vp, _vp, _vp]),
     "ck_quantize_cols": (_int, [_vp, _i64, _int, _int, _flt, _vp, _vp, _vp]),
+    "ck_hbm_copy": (_int, [_vp, _vp, _i64, _int, _vp]),
 }
 
 

@@ -22,6 +22,9 @@
  *   ck_quantize_rows          <- vllm_integration/quantized_packed_decode.py:347-351
  *                                (init_quantized_state seeding from h0)
  *   ck_quantize_cols          <- statequant/kernel.py:99-113 (per_v_channel_quantize)
+ *   ck_hbm_copy               <- measurement only: the device-to-device copy that
+ *                                experiments/cuda_bench.py:39-60 times as the
+ *                                measured bandwidth peak
  */
 #ifndef CARRYKERNEL_GDN_H_
 #define CARRYKERNEL_GDN_H_
@@ -163,6 +166,14 @@ int ck_quantize_rows(const void* x, int x_dtype, int64_t stride_row, int64_t row
  */
 int ck_quantize_cols(const float* x, int64_t M, int K, int V, float qmax,
                      int8_t* codes, float* scale, void* stream);
+
+/*
+ * Measurement only (not on the decode path): copy `bytes` (a multiple of 16;
+ * both pointers 16-byte aligned) from src to dst with a streaming kernel of
+ * `grid` workgroups of 512 threads (0: min(4096, bytes / 8192)). Gives the
+ * measured HBM copy ceiling the decode's bandwidth is compared with.
+ */
+int ck_hbm_copy(const void* src, void* dst, int64_t bytes, int grid, void* stream);
 
 #ifdef __cplusplus
 }

@@ -97,6 +97,11 @@ def test_other_entry_points_argument_errors(L):
     rc = L.ck_gdn_packed_decode_float_state(p, 0, 384, p, 0, 2, p, 0, 2, p, 0, p, 0, 1.0, p, 2, 100, p, 0, p, 1,
                                             4, 1, 1, 2, 128, 64, 0, None)
     assert rc == _native.CK_EINVAL and "float32 or bfloat16" in L.ck_last_error().decode()
+    rc = L.ck_hbm_copy(p, p, 24, 0, None)
+    assert rc == _native.CK_EINVAL and "multiple of 16" in L.ck_last_error().decode()
+    rc = L.ck_hbm_copy(ctypes.c_void_p(8), p, 32, 0, None)
+    assert rc == _native.CK_EINVAL and "aligned" in L.ck_last_error().decode()
+    assert L.ck_hbm_copy(None, None, 0, 0, None) == _native.CK_OK
 
 
 # ---------------------------------------------------------------------------
