@@ -236,10 +236,14 @@ __device__ __forceinline__ void store_resid(int8_t* dst, const uint32_t (&eb)[16
 }
 
 // Stage one item's q and k in LDS buffer `parity`: q * scale and k, both
-// L2-normalised first when the flag is set (each thread computes the norms
-// from the raw values, one division per staged value). qk holds this thread's
-// share of the raw activation bits, element threadIdx.x + j * NT of [q | k].
-// Ends with a barrier after which every thread may read the staged values.
+// L2-normalised first when the flag is set (one division per staged value).
+// qk holds this thread's share of the raw activation bits, element
+// threadIdx.x + j * NT of [q | k]. A thread computes the norm of the vector
+// its element belongs to: the lanes of a row group (LPR lanes) each sum the
+// squares of one 16-element slice in order, then group_sum adds the slices,
+// so every thread of q (or of k) gets the same sum. Threads with no element
+// (a wave past 2K) skip the norm. Ends with a barrier after which every thread
+// may read the staged values.
 template <int K, int QKT, int NT, int ACT>
 __device__ __forceinline__ void stage_qk(const PackedParams& p, const uint32_t (&qk)[QKT], int c, int parity,
                                          float (*s_qk)[2 * K]) {
@@ -253,33 +257,26 @@ __device__ __forceinline__ void stage_qk(const PackedParams& p, const uint32_t (
       if (e < 2 * K) raw[e] = act_decode<ACT>(qk[j]);
     }
     __syncthreads();
-    float sq, sk;
-    {
-      const float4* q4 = reinterpret_cast<const float4*>(raw + c * 16);
-      const float4* k4 = reinterpret_cast<const float4*>(raw + K + c * 16);
-      float qv[16], kv[16];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float4 a4 = q4[j], b4 = k4[j];
-        qv[4 * j] = a4.x, qv[4 * j + 1] = a4.y, qv[4 * j + 2] = a4.z, qv[4 * j + 3] = a4.w;
-        kv[4 * j] = b4.x, kv[4 * j + 1] = b4.y, kv[4 * j + 2] = b4.z, kv[4 * j + 3] = b4.w;
-      }
-      sq = qv[0] * qv[0];
-      sk = kv[0] * kv[0];
-#pragma unroll
-      for (int j = 1; j < 16; ++j) {
-        sq = fmaf(qv[j], qv[j], sq);
-        sk = fmaf(kv[j], kv[j], sk);
-      }
-    }
-    sq = group_sum<LPR>(sq);
-    sk = group_sum<LPR>(sk);
-    const float dq = sqrtf(sq + 1e-6f);
-    const float dk = sqrtf(sk + 1e-6f);
 #pragma unroll
     for (int j = 0; j < QKT; ++j) {
       const int e = (int)threadIdx.x + j * NT;
-      if (e < 2 * K) buf[e] = (e < K) ? (raw[e] / dq) * p.scale : raw[e] / dk;
+      // uniform over a wave for all but its last partial group of elements
+      if ((int)(threadIdx.x & ~63u) + j * NT < 2 * K) {
+        const bool isq = e < K;
+        const float4* x4 = reinterpret_cast<const float4*>(raw + (isq ? 0 : K) + c * 16);
+        float xv[16];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float4 a4 = x4[t];
+          xv[4 * t] = a4.x, xv[4 * t + 1] = a4.y, xv[4 * t + 2] = a4.z, xv[4 * t + 3] = a4.w;
+        }
+        float ss = xv[0] * xv[0];
+#pragma unroll
+        for (int t = 1; t < 16; ++t) ss = fmaf(xv[t], xv[t], ss);
+        ss = group_sum<LPR>(ss);
+        const float d = sqrtf(ss + 1e-6f);
+        if (e < 2 * K) buf[e] = isq ? (raw[e] / d) * p.scale : raw[e] / d;
+      }
     }
   } else {
 #pragma unroll
