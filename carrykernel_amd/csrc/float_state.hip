@@ -175,43 +175,44 @@ void float_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx) 
   const int wave = threadIdx.x >> 6;
   const int c = lane % L::LPR;
   const int g = lane / L::LPR;
-  const int stride = (int)gridDim.x;
-  int item = (int)blockIdx.x;
-  if (item >= p.items) return;  // whole workgroup
+  const pd::WorkSeq w = pd::work_seq(p.items, p.split8);
+  if (w.count <= 0) return;  // whole workgroup
+  int item = w.first;
   const int last = p.items - 1;
+  const int item_end = w.first + w.count * w.step;  // one past this workgroup's last item
   // q/k staging buffers alternate between consecutive live items (see
   // packed_decode_kernel)
   FloatItemRegs<RPL, L::QKT, BF16> A, B;
   ItemCoord ca = pd::item_coord(p, idx, item), cb;
   load_fitem<K, RPL, WAVES, BF16, ACT>(p, ca, true, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, A);
   float alpha_v, beta_v;
-  pd::gates_for_items(p, 0, lane, alpha_v, beta_v);
+  pd::gates_for_items(p, w, 0, lane, alpha_v, beta_v);
   int k = 0, live = 0;
   for (;;) {
-    int next = item + stride;
+    int next = item + w.step;
     cb = pd::item_coord(p, idx, min(next, last));
-    load_fitem<K, RPL, WAVES, BF16, ACT>(p, cb, next < p.items, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, B);
+    load_fitem<K, RPL, WAVES, BF16, ACT>(p, cb, next < item_end, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, B);
     process_fitem<K, RPL, WAVES, BF16, ACT>(p, ca, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, live & 1,
                                             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), k & 63)),
                                             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(beta_v), k & 63)),
                                             A, s_qk);
     live += ca.live ? 1 : 0;
-    if (next >= p.items) break;
+    if (next >= item_end) break;
     ++k;
-    if ((k & 63) == 0) pd::gates_for_items(p, k, lane, alpha_v, beta_v);
+    if ((k & 63) == 0) pd::gates_for_items(p, w, k, lane, alpha_v, beta_v);
     item = next;
 
-    next = item + stride;
+    next = item + w.step;
     ca = pd::item_coord(p, idx, min(next, last));
-    load_fitem<K, RPL, WAVES, BF16, ACT>(p, ca, next < p.items, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, A);
+    load_fitem<K, RPL, WAVES, BF16, ACT>(p, ca, next < item_end, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, A);
     process_fitem<K, RPL, WAVES, BF16, ACT>(p, cb, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, live & 1,
                                             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), k & 63)),
                                             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(beta_v), k & 63)),
                                             B, s_qk);
     live += cb.live ? 1 : 0;
-    if (next >= p.items) break;
+    if (next >= item_end) break;
     ++k;
-    if ((k & 63) == 0) pd::gates_for_items(p, k, lane, alpha_v, beta_v);
+    if ((k & 63) == 0) pd::gates_for_items(p, w, k, lane, alpha_v, beta_v);
     item = next;
   }
 }
@@ -228,10 +229,12 @@ int launch_fs(PackedParams p, int B, hipStream_t stream) {
   p.div_nvt = pd::make_fastdiv((uint32_t)nvt);
   p.div_hv = pd::make_fastdiv((uint32_t)p.HV);
   auto fn = float_decode_kernel<K, RPL, WAVES, BF16, ACT>;
-  const int resident = pd::resident_workgroups(reinterpret_cast<const void*>(fn), WAVES * 64);
+  int per_cu = 0;
+  const int resident = pd::resident_workgroups(reinterpret_cast<const void*>(fn), WAVES * 64, &per_cu);
   if (resident <= 0) return fail(CK_ELAUNCH, "cannot query the device occupancy");
   const int per_wg = (p.items + resident - 1) / resident;
   const int grid = (p.items + per_wg - 1) / per_wg;
+  p.split8 = (per_cu == 2 && grid == resident) ? pd::kPairSplit8 : 0;
   hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(WAVES * 64), 0, stream, p, p.idx);
   return check_launch("ck_gdn_packed_decode_float_state");
 }

@@ -10,13 +10,14 @@
 namespace ck {
 namespace pd {
 
-int resident_workgroups(const void* fn, int block) {
+int resident_workgroups(const void* fn, int block, int* per_cu_out) {
   static std::mutex mu;
   struct Entry {
     const void* fn;
     int device;
     int block;
     int n;
+    int per_cu;
   };
   static Entry cache[512];
   static int ncache = 0;
@@ -24,12 +25,16 @@ int resident_workgroups(const void* fn, int block) {
   if (hipGetDevice(&device) != hipSuccess) return -1;
   std::lock_guard<std::mutex> lock(mu);
   for (int i = 0; i < ncache; ++i)
-    if (cache[i].fn == fn && cache[i].device == device && cache[i].block == block) return cache[i].n;
+    if (cache[i].fn == fn && cache[i].device == device && cache[i].block == block) {
+      if (per_cu_out) *per_cu_out = cache[i].per_cu;
+      return cache[i].n;
+    }
   int per_cu = 0, cus = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, block, 0) != hipSuccess || per_cu <= 0) return -1;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0) return -1;
   const int n = per_cu * cus;
-  if (ncache < 512) cache[ncache++] = {fn, device, block, n};
+  if (ncache < 512) cache[ncache++] = {fn, device, block, n, per_cu};
+  if (per_cu_out) *per_cu_out = per_cu;
   return n;
 }
 

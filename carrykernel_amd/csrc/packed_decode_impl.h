@@ -89,6 +89,7 @@ struct PackedParams {
   int32_t H, HV, V;
   int32_t items;          // B * HV * nvt
   int32_t l2norm;
+  int32_t split8;         // CU-pair split of the items, in eighths (0: plain stride); see work_seq
   FastDiv div_nvt, div_hv;  // nvt = V-tiles per (request, head)
 
   __device__ __forceinline__ int mixed_dtype() const { return dtypes & 15; }
@@ -475,13 +476,63 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
   }
 }
 
+// The items of one workgroup: first, first + step, ... (count of them).
+struct WorkSeq {
+  int first, step, count;
+};
+
+// Item sequence of this workgroup. Plain: blockIdx.x + j * gridDim.x.
+//
+// Split (split8 > 0, an even grid of two resident workgroups per CU, and at
+// least two items per workgroup): the dispatcher places one workgroup on
+// every CU before it fills the second slot, so workgroups b and b + G/2 share
+// a CU, and the instruction arbiter issues from the older waves first.
+// Measured on MI355X (per-workgroup timestamps of one launch), the first-
+// dispatched workgroup of each pair then computes an item in about half the
+// time of its partner and, with an even split, finishes long before it,
+// after which the partner runs alone on the CU at half the CU's wave count.
+// So pair q = b mod G/2 shares the items q + j * G/2 (j = 0 .. n-1) unevenly:
+// the first-dispatched workgroup takes j < ceil(n * split8 / 8), its partner
+// the rest. Any split is correct (each item is taken exactly once); the
+// ratio only changes when the two finish.
+__device__ __forceinline__ WorkSeq work_seq(int items, int split8) {
+  const int G = (int)gridDim.x;
+  const int b = (int)blockIdx.x;
+  WorkSeq w;
+  if (split8 > 0 && (G & 1) == 0 && items >= 2 * G) {
+    const int half = G >> 1;
+    const int q = b < half ? b : b - half;
+    const int n = (items - q + half - 1) / half;
+    const int n_first = (n * split8 + 7) / 8;
+    const int j0 = b < half ? 0 : n_first;
+    const int j1 = b < half ? n_first : n;
+    w.first = q + j0 * half;
+    w.step = half;
+    w.count = j1 - j0;
+  } else {
+    w.first = b;
+    w.step = G;
+    w.count = b < items ? (items - b + G - 1) / G : 0;
+  }
+  w.first = __builtin_amdgcn_readfirstlane(w.first);
+  w.step = __builtin_amdgcn_readfirstlane(w.step);
+  w.count = __builtin_amdgcn_readfirstlane(w.count);
+  return w;
+}
+
+// Share of a CU pair's items taken by its first-dispatched workgroup, in
+// eighths, for kernels resident two workgroups per CU (5/8: the measured
+// per-item times of the two workgroups are in a ratio of about 5:3 on the
+// int4 per-head step; 5/8 to 2/3 all gave the same step time).
+constexpr int kPairSplit8 = 5;
+
 // Gates of this workgroup's items number kbase .. kbase+63 (one per lane).
-__device__ __forceinline__ void gates_for_items(const PackedParams& p, int kbase, int lane, float& alpha_v,
-                                                float& beta_v) {
+__device__ __forceinline__ void gates_for_items(const PackedParams& p, const WorkSeq& w, int kbase, int lane,
+                                                float& alpha_v, float& beta_v) {
   // Branch-free over lanes (lanes past the last item recompute the last
   // item's gates, which are never read): a divergent region here would move
   // the uniform dtype/stride values into VGPRs that stay live over the loop.
-  const int item = min((int)blockIdx.x + (kbase + lane) * (int)gridDim.x, p.items - 1);
+  const int item = min(w.first + (kbase + lane) * w.step, p.items - 1);
   const uint32_t nh = fdiv((uint32_t)item, p.div_nvt);
   const uint32_t n = fdiv(nh, p.div_hv);
   const int hv = (int)(nh - n * p.div_hv.d);
@@ -508,11 +559,12 @@ void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx)
   const int wave = threadIdx.x >> 6;
   const int c = lane % L::LPR;
   const int g = lane / L::LPR;
-  const int stride = (int)gridDim.x;
 
-  int item = (int)blockIdx.x;
-  if (item >= p.items) return;  // whole workgroup
+  const WorkSeq w = work_seq(p.items, p.split8);
+  if (w.count <= 0) return;  // whole workgroup
+  int item = w.first;
   const int last = p.items - 1;
+  const int item_end = w.first + w.count * w.step;  // one past this workgroup's last item
 
   // LDS buffers alternate between consecutive live items (a NULL item skips
   // the barriers, so the parity follows a count of live items): two uses of
@@ -521,14 +573,14 @@ void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx)
   ItemCoord ca = item_coord(p, idx, item), cb;
   load_item<K, RPL, WAVES, RESID, PER_HEAD, ACT>(p, ca, true, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, A);
   float alpha_v, beta_v;
-  gates_for_items(p, 0, lane, alpha_v, beta_v);  // its loads overlap the first item's
+  gates_for_items(p, w, 0, lane, alpha_v, beta_v);  // its loads overlap the first item's
   int k = 0;     // item number within this workgroup
   int live = 0;  // live items processed so far
   for (;;) {
     // ---- item k in A; prefetch item k+1 into B (past the end: re-read the last item) ----
-    int next = item + stride;
+    int next = item + w.step;
     cb = item_coord(p, idx, min(next, last));
-    load_item<K, RPL, WAVES, RESID, PER_HEAD, ACT>(p, cb, next < p.items, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, B);
+    load_item<K, RPL, WAVES, RESID, PER_HEAD, ACT>(p, cb, next < item_end, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, B);
     {
       const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), k & 63));
       const float beta = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(beta_v), k & 63));
@@ -536,15 +588,15 @@ void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx)
                                                           lane, wave, live & 1, alpha, beta, A, s_qk, s_red, s_ek);
       live += ca.live ? 1 : 0;
     }
-    if (next >= p.items) break;
+    if (next >= item_end) break;
     ++k;
-    if ((k & 63) == 0) gates_for_items(p, k, lane, alpha_v, beta_v);
+    if ((k & 63) == 0) gates_for_items(p, w, k, lane, alpha_v, beta_v);
     item = next;
 
     // ---- item k in B; prefetch item k+1 into A ----
-    next = item + stride;
+    next = item + w.step;
     ca = item_coord(p, idx, min(next, last));
-    load_item<K, RPL, WAVES, RESID, PER_HEAD, ACT>(p, ca, next < p.items, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, A);
+    load_item<K, RPL, WAVES, RESID, PER_HEAD, ACT>(p, ca, next < item_end, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, A);
     {
       const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), k & 63));
       const float beta = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(beta_v), k & 63));
@@ -552,15 +604,16 @@ void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx)
                                                           lane, wave, live & 1, alpha, beta, B, s_qk, s_red, s_ek);
       live += cb.live ? 1 : 0;
     }
-    if (next >= p.items) break;
+    if (next >= item_end) break;
     ++k;
-    if ((k & 63) == 0) gates_for_items(p, k, lane, alpha_v, beta_v);
+    if ((k & 63) == 0) gates_for_items(p, w, k, lane, alpha_v, beta_v);
     item = next;
   }
 }
 
-// Resident workgroups per GPU for a kernel (occupancy x CUs), cached per device.
-int resident_workgroups(const void* fn, int block);
+// Resident workgroups per GPU for a kernel (occupancy x CUs), cached per
+// device; *per_cu (if given) receives the occupancy per CU.
+int resident_workgroups(const void* fn, int block, int* per_cu = nullptr);
 
 template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ACT>
 int launch_cfg(PackedParams p, int B, hipStream_t stream) {
@@ -573,11 +626,13 @@ int launch_cfg(PackedParams p, int B, hipStream_t stream) {
   p.div_nvt = make_fastdiv((uint32_t)nvt);
   p.div_hv = make_fastdiv((uint32_t)p.HV);
   auto fn = packed_decode_kernel<K, RPL, WAVES, RESID, PER_HEAD, MODE, ACT>;
-  const int resident = resident_workgroups(reinterpret_cast<const void*>(fn), WAVES * 64);
+  int per_cu = 0;
+  const int resident = resident_workgroups(reinterpret_cast<const void*>(fn), WAVES * 64, &per_cu);
   if (resident <= 0) return fail(CK_ELAUNCH, "cannot query the device occupancy");
   // fewest items per workgroup, then the fewest workgroups achieving it
   const int per_wg = (p.items + resident - 1) / resident;
   const int grid = (p.items + per_wg - 1) / per_wg;
+  p.split8 = (per_cu == 2 && grid == resident) ? kPairSplit8 : 0;
   hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(WAVES * 64), 0, stream, p, p.idx);
   return check_launch("ck_gdn_packed_decode");
 }

@@ -60,6 +60,18 @@ def test_bit_exact_vs_oracle_k128(device, resid_fmt, per_head, mode):
               mode=mode, l2norm=False, T=3)
 
 
+@pytest.mark.parametrize("resid_fmt", [qpd.RESID_INT8, qpd.RESID_INT4])
+@pytest.mark.parametrize("per_head", [False, True])
+@pytest.mark.parametrize("B", [64, 37])
+def test_bit_exact_full_occupancy(device, resid_fmt, per_head, B):
+    """Batches with at least two items per resident workgroup: the per-head
+    step splits each CU pair's items unevenly between its two workgroups
+    (B=37: pairs with different item counts), the per-row step runs four
+    workgroups per CU."""
+    _run_both(device, B=B, H=32, HV=32, K=128, V=128, resid_fmt=resid_fmt, per_head=per_head,
+              mode="fast", l2norm=False, T=2)
+
+
 @pytest.mark.parametrize("K,V,H,HV", [(64, 64, 8, 16), (32, 8, 4, 4), (32, 4, 1, 1), (16, 40, 2, 2),
                                       (256, 128, 2, 4), (128, 200, 1, 2)])
 @pytest.mark.parametrize("resid_fmt", [qpd.RESID_INT8, qpd.RESID_INT4])
