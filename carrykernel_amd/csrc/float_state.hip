@@ -175,7 +175,7 @@ void float_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx) 
   const int wave = threadIdx.x >> 6;
   const int c = lane % L::LPR;
   const int g = lane / L::LPR;
-  const pd::WorkSeq w = pd::work_seq(p.items, p.split8);
+  const pd::WorkSeq w = pd::work_seq(p.items, p.cu_share_n, p.cu_shares);
   if (w.count <= 0) return;  // whole workgroup
   int item = w.first;
   const int last = p.items - 1;
@@ -234,7 +234,7 @@ int launch_fs(PackedParams p, int B, hipStream_t stream) {
   if (resident <= 0) return fail(CK_ELAUNCH, "cannot query the device occupancy");
   const int per_wg = (p.items + resident - 1) / resident;
   const int grid = (p.items + per_wg - 1) / per_wg;
-  p.split8 = (per_cu == 2 && grid == resident) ? pd::kPairSplit8 : 0;
+  pd::set_cu_shares(p, grid, resident, per_cu);
   hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(WAVES * 64), 0, stream, p, p.idx);
   return check_launch("ck_gdn_packed_decode_float_state");
 }

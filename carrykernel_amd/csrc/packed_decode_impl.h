@@ -89,7 +89,8 @@ struct PackedParams {
   int32_t H, HV, V;
   int32_t items;          // B * HV * nvt
   int32_t l2norm;
-  int32_t split8;         // CU-pair split of the items, in eighths (0: plain stride); see work_seq
+  int32_t cu_share_n;     // workgroups per CU that share their items unevenly (<= 1: plain stride); see work_seq
+  uint32_t cu_shares;     // byte a: share of the age-a workgroup, in 64ths
   FastDiv div_nvt, div_hv;  // nvt = V-tiles per (request, head)
 
   __device__ __forceinline__ int mixed_dtype() const { return dtypes & 15; }
@@ -483,32 +484,36 @@ struct WorkSeq {
 
 // Item sequence of this workgroup. Plain: blockIdx.x + j * gridDim.x.
 //
-// Split (split8 > 0, an even grid of two resident workgroups per CU, and at
-// least two items per workgroup): the dispatcher places one workgroup on
-// every CU before it fills the second slot, so workgroups b and b + G/2 share
-// a CU, and the instruction arbiter issues from the older waves first.
-// Measured on MI355X (per-workgroup timestamps of one launch), the first-
-// dispatched workgroup of each pair then computes an item in about half the
-// time of its partner and, with an even split, finishes long before it,
-// after which the partner runs alone on the CU at half the CU's wave count.
-// So pair q = b mod G/2 shares the items q + j * G/2 (j = 0 .. n-1) unevenly:
-// the first-dispatched workgroup takes j < ceil(n * split8 / 8), its partner
-// the rest. Any split is correct (each item is taken exactly once); the
-// ratio only changes when the two finish.
-__device__ __forceinline__ WorkSeq work_seq(int items, int split8) {
+// Shared (P = cu_share_n > 1 resident workgroups per CU, a grid of P x CUs,
+// at least two items per workgroup): the dispatcher places one workgroup on
+// every CU before it fills the next slot, so with m = G / P the workgroups
+// q, q + m, ..., q + (P-1) m share a CU, in order of age a = b / m, and the
+// instruction arbiter issues from the oldest waves first. Measured on MI355X
+// (per-workgroup timestamps of one launch) an older workgroup computes an
+// item in a fraction of a younger one's time; with an even split the older
+// ones finish first and the last ones run alone at a fraction of the CU's
+// wave count. So the group's items q + j m (j = 0 .. n-1) are shared
+// unevenly: age a takes the j from ceil(n * c_a / 64) up to the next age's
+// start, where c_a is the sum of the shares (bytes of cu_shares) of the
+// older ages. Any shares are correct (each item is taken exactly once); they
+// only change when the workgroups of a CU finish.
+__device__ __forceinline__ WorkSeq work_seq(int items, int share_n, uint32_t shares) {
   const int G = (int)gridDim.x;
   const int b = (int)blockIdx.x;
   WorkSeq w;
-  if (split8 > 0 && (G & 1) == 0 && items >= 2 * G) {
-    const int half = G >> 1;
-    const int q = b < half ? b : b - half;
-    const int n = (items - q + half - 1) / half;
-    const int n_first = (n * split8 + 7) / 8;
-    const int j0 = b < half ? 0 : n_first;
-    const int j1 = b < half ? n_first : n;
-    w.first = q + j0 * half;
-    w.step = half;
-    w.count = j1 - j0;
+  if (share_n > 1 && G % share_n == 0 && items >= 2 * G) {
+    const int m = G / share_n;
+    const int age = b / m;
+    const int q = b - age * m;
+    const int n = (items - q + m - 1) / m;
+    int c_lo = 0;
+    for (int a = 0; a < age; ++a) c_lo += (int)((shares >> (8 * a)) & 0xffu);
+    const int c_hi = c_lo + (int)((shares >> (8 * age)) & 0xffu);
+    const int j0 = (n * c_lo + 63) / 64;
+    const int j1 = age == share_n - 1 ? n : (n * c_hi + 63) / 64;
+    w.first = q + j0 * m;
+    w.step = m;
+    w.count = max(j1 - j0, 0);
   } else {
     w.first = b;
     w.step = G;
@@ -520,11 +525,31 @@ __device__ __forceinline__ WorkSeq work_seq(int items, int split8) {
   return w;
 }
 
-// Share of a CU pair's items taken by its first-dispatched workgroup, in
-// eighths, for kernels resident two workgroups per CU (5/8: the measured
-// per-item times of the two workgroups are in a ratio of about 5:3 on the
-// int4 per-head step; 5/8 to 2/3 all gave the same step time).
-constexpr int kPairSplit8 = 5;
+// Shares (64ths, byte a = age a) for two and for four resident workgroups
+// per CU, from the per-age item times measured on the int4 steps: two 8-wave
+// workgroups (per-head residual scale) about 5:3; four 4-wave workgroups
+// (per-row residual scale) about 19:17:15:13.
+#ifndef CK_CU_SHARES2
+#define CK_CU_SHARES2 (40u | (24u << 8))
+#endif
+#ifndef CK_CU_SHARES4
+#define CK_CU_SHARES4 (19u | (17u << 8) | (15u << 16) | (13u << 24))
+#endif
+
+// Sets the item sharing of a persistent launch of `grid` workgroups, given
+// the kernel's occupancy per CU and the resident grid.
+inline void set_cu_shares(PackedParams& p, int grid, int resident, int per_cu) {
+  p.cu_share_n = 0;
+  p.cu_shares = 0;
+  if (grid != resident) return;
+  if (per_cu == 2) {
+    p.cu_share_n = 2;
+    p.cu_shares = CK_CU_SHARES2;
+  } else if (per_cu == 4) {
+    p.cu_share_n = 4;
+    p.cu_shares = CK_CU_SHARES4;
+  }
+}
 
 // Gates of this workgroup's items number kbase .. kbase+63 (one per lane).
 __device__ __forceinline__ void gates_for_items(const PackedParams& p, const WorkSeq& w, int kbase, int lane,
@@ -560,7 +585,7 @@ void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx)
   const int c = lane % L::LPR;
   const int g = lane / L::LPR;
 
-  const WorkSeq w = work_seq(p.items, p.split8);
+  const WorkSeq w = work_seq(p.items, p.cu_share_n, p.cu_shares);
   if (w.count <= 0) return;  // whole workgroup
   int item = w.first;
   const int last = p.items - 1;
@@ -632,7 +657,7 @@ int launch_cfg(PackedParams p, int B, hipStream_t stream) {
   // fewest items per workgroup, then the fewest workgroups achieving it
   const int per_wg = (p.items + resident - 1) / resident;
   const int grid = (p.items + per_wg - 1) / per_wg;
-  p.split8 = (per_cu == 2 && grid == resident) ? kPairSplit8 : 0;
+  set_cu_shares(p, grid, resident, per_cu);
   hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(WAVES * 64), 0, stream, p, p.idx);
   return check_launch("ck_gdn_packed_decode");
 }
