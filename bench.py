@@ -479,6 +479,78 @@ def drift_c5(device, bits, tokens=2048, layers=24, B=64, every=256, resid_fmt=No
     return rows
 
 
+def timeline_report(device, B, resid_fmt, per_head, groups, launches=20):
+    """Per-workgroup timeline of one launch of the headline step, from the
+    timestamped measurement build (libcarrykernel_gdn_timeline.so): the last
+    of `launches` back-to-back eager launches writes, for every workgroup, its
+    start, and per item the times its processing began, its loads had all
+    landed, and its stores were issued (s_memrealtime, 100 MHz), plus the CU
+    it ran on. Returns per-age statistics (age = dispatch order among the
+    workgroups that share a CU)."""
+    import numpy as np
+    from carrykernel_amd import _native
+    L = _native.use_timeline_build()
+    S = B * groups + 1
+    state = warm_state(S, device, 0)
+    pool = qpd.init_quantized_state(S, HV, V, K, device, h0=state, resid_fmt=resid_fmt,
+                                    per_head_resid_scale=per_head)
+    del state
+    sets, A_log, dt_bias = make_step_inputs(B, 8, device, 1)
+    perm = torch.randperm(S - 1, generator=torch.Generator().manual_seed(0)) + 1
+    ids = [perm[i * B:(i + 1) * B].to(torch.int32).to(device) for i in range(groups)]
+    out = torch.empty(B, 1, HV, V, device=device)
+
+    def step(t):
+        mixed, a, b = sets[t % len(sets)]
+        qpd.quantized_gated_delta_rule_packed_decode(mixed, a, b, A_log, dt_bias, 1.0, *pool, out, ids[t % groups],
+                                                    resid_fmt=resid_fmt)
+
+    for t in range(200):
+        step(t)
+    torch.cuda.synchronize()
+    slots, max_wg = 32, 2048
+    buf = torch.zeros(max_wg * slots, dtype=torch.int64, device=device)
+    _native.check(L.ck_timeline_set(buf.data_ptr()), "ck_timeline_set")
+    for t in range(launches - 1):
+        step(t)
+    buf.zero_()                      # on the launch stream, between the last two launches
+    step(launches - 1)
+    torch.cuda.synchronize()
+    _native.check(L.ck_timeline_set(None), "ck_timeline_set")
+    ts = buf.cpu().numpy().view(np.uint64).reshape(max_wg, slots)
+    nwg = int(np.count_nonzero(ts[:, 0]))
+    t = ts[:nwg, :31].astype(np.int64)
+    t0 = t[:, 0].min()
+    rel = np.where(t > 0, (t - t0) * 1e-2, np.nan)          # us
+    hw = (ts[:nwg, 31] & 0xffffffff).astype(np.int64)
+    xcc = (ts[:nwg, 31] >> 32).astype(np.int64) & 0xf
+    cu_id = xcc * 1024 + ((hw >> 13) & 7) * 64 + ((hw >> 12) & 1) * 16 + ((hw >> 8) & 0xf)
+    per_cu = int(np.bincount(np.unique(cu_id, return_inverse=True)[1]).max())
+    begin, data, end = rel[:, 1:31:3], rel[:, 2:31:3], rel[:, 3:31:3]
+    n_rec = np.sum(~np.isnan(end), axis=1)
+    last_end = np.array([end[i, n_rec[i] - 1] for i in range(nwg)])
+    comp = np.nansum(end - data, axis=1) / n_rec
+    wait = np.nansum(data - begin, axis=1) / n_rec
+    m = nwg // per_cu
+    ages = []
+    for a in range(per_cu):
+        sel = slice(a * m, (a + 1) * m)
+        ages.append({"age": a, "items_median": float(np.median(n_rec[sel])),
+                     "first_data_us": round(float(np.median(data[sel, 0])), 2),
+                     "compute_us_per_item": round(float(np.median(comp[sel])), 2),
+                     "wait_us_per_item": round(float(np.median(wait[sel])), 2),
+                     "end_us_median": round(float(np.median(last_end[sel])), 2),
+                     "end_us_max": round(float(np.max(last_end[sel])), 2)})
+    return {"timeline": {"workload": f"B={B} {'int4' if resid_fmt == qpd.RESID_INT4 else 'int8'} residual, "
+                                     f"{'per-head' if per_head else 'per-row'} scale",
+                         "workgroups": nwg, "workgroups_per_cu": per_cu,
+                         "span_us": round(float(np.nanmax(last_end)), 2),
+                         "end_us_median": round(float(np.median(last_end)), 2),
+                         "end_us_p90": round(float(np.percentile(last_end, 90)), 2),
+                         "ages": ages,
+                         "note": "items >= 10 per workgroup are counted as 10 (the buffer keeps 10 item slots)"}}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -500,6 +572,9 @@ def main():
                          "against the fp32 state arm; prints one JSON line")
     ap.add_argument("--drift-tokens", type=int, default=2048)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--timeline", action="store_true",
+                    help="instead: per-workgroup timeline of one launch of the chosen step from the "
+                         "timestamped measurement build (prints one JSON line)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="instead: time a plain device copy of this many MiB (HBM copy peak, and the "
                          "byte-count calibration for the FETCH_SIZE / WRITE_SIZE counters)")
@@ -530,6 +605,9 @@ def main():
     resid_fmt = qpd.RESID_INT4 if args.resid == "int4" else qpd.RESID_INT8
     per_head = args.rscale == "head"
     B = args.batch
+    if args.timeline:
+        print(json.dumps(timeline_report(device, B, resid_fmt, per_head, max(2, min(64, 1024 // B)))), flush=True)
+        return
 
     ms, host_ms = run_config(device, B, resid_fmt, per_head, args.steps, args.warmup, args.groups,
                              args.quant_mode)

@@ -19,6 +19,9 @@ import torch
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG_DIR, "lib", "libcarrykernel_gdn.so")
+# measurement build of the same sources with per-workgroup timestamps
+# (CK_TIMELINE); loaded only by use_timeline_build()
+TIMELINE_LIB_PATH = os.path.join(PKG_DIR, "lib", "libcarrykernel_gdn_timeline.so")
 
 ABI_VERSION = 1
 
@@ -109,6 +112,22 @@ def lib():
                 raise HipUnavailable("libcarrykernel_gdn.so ABI version mismatch; rebuild it")
             _lib = L
     return _lib
+
+
+def use_timeline_build():
+    """Measurement only: load the timeline build instead of the product
+    library (must come before anything else loads the library). Its decode
+    launches write per-workgroup timestamps to the buffer given to
+    ``ck_timeline_set`` (see packed_decode_impl.h)."""
+    global LIB_PATH
+    with _lock:
+        if _lib is not None and LIB_PATH != TIMELINE_LIB_PATH:
+            raise RuntimeError("the product library is already loaded in this process")
+        LIB_PATH = TIMELINE_LIB_PATH
+    L = lib()
+    L.ck_timeline_set.restype = _int
+    L.ck_timeline_set.argtypes = [_vp]
+    return L
 
 
 def exported_symbols() -> list[str]:

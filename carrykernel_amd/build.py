@@ -22,6 +22,7 @@ INCLUDE_DIR = os.path.join(REPO_DIR, "include")
 LIB_DIR = os.path.join(PKG_DIR, "lib")
 LIB_NAME = "libcarrykernel_gdn.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
+TIMELINE_LIB_PATH = os.path.join(LIB_DIR, "libcarrykernel_gdn_timeline.so")
 OBJ_DIR = os.path.join(LIB_DIR, "_obj")
 
 ARCH = "gfx950"
@@ -63,14 +64,20 @@ def _run(cmd: list[str]) -> str:
     return err
 
 
-def build(verbose: bool = False, extra_flags: list[str] | None = None, jobs: int | None = None) -> str:
+def build(verbose: bool = False, extra_flags: list[str] | None = None, jobs: int | None = None,
+          timeline: bool = False) -> str:
     """Compile every source (in parallel) and link the library; returns its
-    path. Always recompiles."""
-    os.makedirs(OBJ_DIR, exist_ok=True)
+    path. Always recompiles. ``timeline=True`` builds the measurement variant
+    (``CK_TIMELINE``: per-workgroup timestamps in the decode kernel) as
+    ``libcarrykernel_gdn_timeline.so`` beside the product library."""
+    obj_dir = OBJ_DIR + ("_timeline" if timeline else "")
+    lib_path = TIMELINE_LIB_PATH if timeline else LIB_PATH
+    os.makedirs(obj_dir, exist_ok=True)
     hipcc = hipcc_path()
-    flags = [*HIPCC_FLAGS, *(extra_flags or []), f"-I{INCLUDE_DIR}", f"-I{CSRC_DIR}"]
+    flags = [*HIPCC_FLAGS, *(["-DCK_TIMELINE=1"] if timeline else []), *(extra_flags or []),
+             f"-I{INCLUDE_DIR}", f"-I{CSRC_DIR}"]
     srcs = sources()
-    objs = [os.path.join(OBJ_DIR, os.path.basename(f)[:-4] + ".o") for f in srcs]
+    objs = [os.path.join(obj_dir, os.path.basename(f)[:-4] + ".o") for f in srcs]
     cmds = [[hipcc, *flags, "-c", src, "-o", obj] for src, obj in zip(srcs, objs)]
     jobs = jobs or max(1, min(16, len(os.sched_getaffinity(0))))
     with ThreadPoolExecutor(max_workers=jobs) as pool:
@@ -79,14 +86,14 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None, jobs: int
                 print(" ".join(cmd), flush=True)
                 if err.strip():
                     print(err, file=sys.stderr)
-    tmp = LIB_PATH + ".tmp"
+    tmp = lib_path + ".tmp"
     link = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     if verbose:
         print(" ".join(link), flush=True)
     _run(link)
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, lib_path)
+    return lib_path
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose=True, timeline="--timeline" in sys.argv[1:]))

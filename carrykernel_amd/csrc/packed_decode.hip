@@ -41,6 +41,10 @@ int resident_workgroups(const void* fn, int block, int* per_cu_out) {
 }  // namespace pd
 }  // namespace ck
 
+#if CK_TIMELINE
+static void* g_timeline = nullptr;
+#endif
+
 extern "C" int ck_gdn_packed_decode(const void* mixed_qkv, int qkv_dtype, int64_t stride_qkv_tok,
                                     const void* a, int a_dtype, int64_t stride_a_tok,
                                     const void* b, int b_dtype, int64_t stride_b_tok,
@@ -128,6 +132,9 @@ extern "C" int ck_gdn_packed_decode(const void* mixed_qkv, int qkv_dtype, int64_
   p.HV = HV;
   p.V = V;
   p.l2norm = use_qk_l2norm ? 1 : 0;
+#if CK_TIMELINE
+  p.timeline = static_cast<uint64_t*>(g_timeline);
+#endif
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int per_head = rscale_mode == CK_RSCALE_PER_HEAD;
   const int mode = quant_mode == CK_QUANT_EXACT ? kExact : kFast;
@@ -143,3 +150,13 @@ extern "C" int ck_gdn_packed_decode(const void* mixed_qkv, int qkv_dtype, int64_
 extern "C" const char* ck_last_error(void) { return ck::last_error().c_str(); }
 
 extern "C" int ck_abi_version(void) { return 1; }
+
+#if CK_TIMELINE
+// Timeline build only: device buffer of kTlMaxWorkgroups x kTlSlots uint64
+// that the following ck_gdn_packed_decode launches write their timestamps to
+// (NULL: none). Not thread-safe; for measurement runs.
+extern "C" int ck_timeline_set(void* device_buffer) {
+  g_timeline = device_buffer;
+  return CK_OK;
+}
+#endif

@@ -91,6 +91,7 @@ struct PackedParams {
   int32_t l2norm;
   int32_t cu_share_n;     // workgroups per CU that share their items unevenly (<= 1: plain stride); see work_seq
   uint32_t cu_shares;     // byte a: share of the age-a workgroup, in 64ths
+  uint64_t* timeline;     // timeline build only (CK_TIMELINE): per-workgroup timestamps, else unused
   FastDiv div_nvt, div_hv;  // nvt = V-tiles per (request, head)
 
   __device__ __forceinline__ int mixed_dtype() const { return dtypes & 15; }
@@ -477,6 +478,59 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
   }
 }
 
+// Timeline build (compiled with CK_TIMELINE=1 into a separate library; the
+// product library has none of this): lane 0 of each workgroup writes
+// s_memrealtime (a 100 MHz counter) into p.timeline[blockIdx.x * kTlSlots + s]:
+// s = 0 at its start; for item k (k >= 9 reuses k = 9's slots) s = 1 + 3k when
+// the item's processing begins, 2 + 3k once all of its loads have landed,
+// 3 + 3k when its stores are issued; s = 31 holds the HW_ID register (low
+// word) and the XCC id (high word) of the CU it ran on.
+constexpr int kTlSlots = 32;
+constexpr int kTlMaxWorkgroups = 2048;
+
+__device__ __forceinline__ void tl_mark(const PackedParams& p, int slot) {
+#if CK_TIMELINE
+  const uint64_t t = __builtin_amdgcn_s_memrealtime();
+  if (p.timeline && threadIdx.x == 0 && blockIdx.x < kTlMaxWorkgroups) p.timeline[blockIdx.x * kTlSlots + slot] = t;
+#else
+  (void)p;
+  (void)slot;
+#endif
+}
+
+__device__ __forceinline__ void tl_start(const PackedParams& p) {
+#if CK_TIMELINE
+  tl_mark(p, 0);
+  if (p.timeline && threadIdx.x == 0 && blockIdx.x < kTlMaxWorkgroups) {
+    const uint32_t hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);    // HW_REG_HW_ID
+    const uint32_t xcc = __builtin_amdgcn_s_getreg((31 << 11) | 20);  // HW_REG_XCC_ID
+    p.timeline[blockIdx.x * kTlSlots + 31] = ((uint64_t)xcc << 32) | hw;
+  }
+#else
+  (void)p;
+#endif
+}
+
+__device__ __forceinline__ int tl_item_slot(int k, int phase) { return 1 + 3 * (k < 9 ? k : 9) + phase; }
+
+// Timeline build: wait until every load of the item in R has landed (the
+// vector memory counter retires in order, so waiting for the last-issued
+// values waits for all of them), then mark.
+template <typename Regs>
+__device__ __forceinline__ void tl_data_ready(const PackedParams& p, int k, const Regs& R) {
+#if CK_TIMELINE
+  constexpr int rpl = sizeof(R.s_in) / sizeof(R.s_in[0]);
+  constexpr int qkt = sizeof(R.qk) / sizeof(R.qk[0]);
+  asm volatile("" ::"v"(R.cw[rpl - 1].w), "v"(R.ew[rpl - 1][0]), "v"(R.qk[qkt - 1]), "v"(R.es_in[0]),
+               "v"(R.vv[rpl - 1]), "v"(R.s_in[rpl - 1]));
+  tl_mark(p, tl_item_slot(k, 1));
+#else
+  (void)p;
+  (void)k;
+  (void)R;
+#endif
+}
+
 // The items of one workgroup: first, first + step, ... (count of them).
 struct WorkSeq {
   int first, step, count;
@@ -584,6 +638,7 @@ void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx)
   const int wave = threadIdx.x >> 6;
   const int c = lane % L::LPR;
   const int g = lane / L::LPR;
+  tl_start(p);
 
   const WorkSeq w = work_seq(p.items, p.cu_share_n, p.cu_shares);
   if (w.count <= 0) return;  // whole workgroup
@@ -609,9 +664,12 @@ void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx)
     {
       const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), k & 63));
       const float beta = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(beta_v), k & 63));
+      tl_mark(p, tl_item_slot(k, 0));
+      tl_data_ready(p, k, A);
       process_item<K, RPL, WAVES, RESID, PER_HEAD, MODE, ACT>(p, ca, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c,
                                                           lane, wave, live & 1, alpha, beta, A, s_qk, s_red, s_ek);
       live += ca.live ? 1 : 0;
+      tl_mark(p, tl_item_slot(k, 2));
     }
     if (next >= item_end) break;
     ++k;
@@ -625,9 +683,12 @@ void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx)
     {
       const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), k & 63));
       const float beta = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(beta_v), k & 63));
+      tl_mark(p, tl_item_slot(k, 0));
+      tl_data_ready(p, k, B);
       process_item<K, RPL, WAVES, RESID, PER_HEAD, MODE, ACT>(p, cb, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c,
                                                           lane, wave, live & 1, alpha, beta, B, s_qk, s_red, s_ek);
       live += cb.live ? 1 : 0;
+      tl_mark(p, tl_item_slot(k, 2));
     }
     if (next >= item_end) break;
     ++k;
