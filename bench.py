@@ -532,6 +532,9 @@ def timeline_report(device, B, resid_fmt, per_head, groups, launches=20):
     comp = np.nansum(end - data, axis=1) / n_rec
     wait = np.nansum(data - begin, axis=1) / n_rec
     m = nwg // per_cu
+    # do the workgroups q, q + m, ... share a CU (for every q)?
+    groups_ok = sum(1 for q in range(m) if len({int(cu_id[q + a * m]) for a in range(per_cu)}) == 1
+                    and int(np.count_nonzero(cu_id == cu_id[q])) == per_cu)
     ages = []
     for a in range(per_cu):
         sel = slice(a * m, (a + 1) * m)
@@ -544,6 +547,7 @@ def timeline_report(device, B, resid_fmt, per_head, groups, launches=20):
     return {"timeline": {"workload": f"B={B} {'int4' if resid_fmt == qpd.RESID_INT4 else 'int8'} residual, "
                                      f"{'per-head' if per_head else 'per-row'} scale",
                          "workgroups": nwg, "workgroups_per_cu": per_cu,
+                         "cu_groups_in_dispatch_order": f"{groups_ok} of {m}",
                          "span_us": round(float(np.nanmax(last_end)), 2),
                          "end_us_median": round(float(np.median(last_end)), 2),
                          "end_us_p90": round(float(np.percentile(last_end, 90)), 2),
