@@ -71,6 +71,22 @@ _SIGNATURES = {
         _int, _int, _int, _int, _int,   # B H HV K V
         _int, _int, _int, _int, _int,   # l2norm resid_fmt rscale_mode bits quant_mode
         _vp]),
+    "ck_gdn_packed_decode_to": (_int, [
+        _vp, _int, _i64, _vp, _int, _i64, _vp, _int, _i64, _vp, _int, _vp, _int, _flt,
+        _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64,
+        _vp, _int,
+        _vp, _i64,                # indices
+        _vp, _i64,                # destination indices
+        _i64,
+        _int, _int, _int, _int, _int,
+        _int, _int, _int, _int, _int,
+        _vp]),
+    "ck_pool_copy_slots": (_int, [
+        _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64,   # source pool
+        _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64,   # destination pool
+        _vp, _vp, _int, _int, _int, _int, _int, _int, _vp]),
+    "ck_pool_reset_slots": (_int, [
+        _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _vp, _int, _int, _int, _int, _int, _int, _vp]),
     "ck_gdn_packed_decode_float_state": (_int, [
         _vp, _int, _i64, _vp, _int, _i64, _vp, _int, _i64, _vp, _int, _vp, _int, _flt,
         _vp, _int, _i64, _vp, _int, _vp, _i64, _i64,

@@ -45,23 +45,26 @@ int resident_workgroups(const void* fn, int block, int* per_cu_out) {
 static void* g_timeline = nullptr;
 #endif
 
-extern "C" int ck_gdn_packed_decode(const void* mixed_qkv, int qkv_dtype, int64_t stride_qkv_tok,
-                                    const void* a, int a_dtype, int64_t stride_a_tok,
-                                    const void* b, int b_dtype, int64_t stride_b_tok,
-                                    const void* A_log, int A_log_dtype,
-                                    const void* dt_bias, int dt_bias_dtype,
-                                    float scale,
-                                    int8_t* state_codes, int64_t stride_state_slot,
-                                    float* state_scale, int64_t stride_sscale_slot,
-                                    int8_t* resid_codes, int64_t stride_resid_slot,
-                                    float* resid_scale, int64_t stride_rscale_slot,
-                                    void* out, int out_dtype,
-                                    const int32_t* ssm_state_indices, int64_t stride_indices,
-                                    int64_t num_slots,
-                                    int B, int H, int HV, int K, int V,
-                                    int use_qk_l2norm, int resid_fmt, int rscale_mode,
-                                    int state_bits, int quant_mode,
-                                    void* stream) {
+// Shared body of ck_gdn_packed_decode (dst_indices == NULL: in place) and
+// ck_gdn_packed_decode_to.
+static int packed_decode_impl(const void* mixed_qkv, int qkv_dtype, int64_t stride_qkv_tok,
+                              const void* a, int a_dtype, int64_t stride_a_tok,
+                              const void* b, int b_dtype, int64_t stride_b_tok,
+                              const void* A_log, int A_log_dtype,
+                              const void* dt_bias, int dt_bias_dtype,
+                              float scale,
+                              int8_t* state_codes, int64_t stride_state_slot,
+                              float* state_scale, int64_t stride_sscale_slot,
+                              int8_t* resid_codes, int64_t stride_resid_slot,
+                              float* resid_scale, int64_t stride_rscale_slot,
+                              void* out, int out_dtype,
+                              const int32_t* ssm_state_indices, int64_t stride_indices,
+                              const int32_t* dst_indices, int64_t stride_dst_indices,
+                              int64_t num_slots,
+                              int B, int H, int HV, int K, int V,
+                              int use_qk_l2norm, int resid_fmt, int rscale_mode,
+                              int state_bits, int quant_mode,
+                              void* stream) {
   using namespace ck;
   using namespace ck::pd;
   if (B < 0 || H <= 0 || HV <= 0 || K <= 0 || V <= 0)
@@ -95,7 +98,7 @@ extern "C" int ck_gdn_packed_decode(const void* mixed_qkv, int qkv_dtype, int64_
     return fail(CK_EUNSUPPORTED, "head or activation row too large");
 
   const int64_t strides[] = {stride_qkv_tok, stride_a_tok, stride_b_tok, stride_state_slot, stride_sscale_slot,
-                             stride_resid_slot, stride_rscale_slot, stride_indices};
+                             stride_resid_slot, stride_rscale_slot, stride_indices, stride_dst_indices};
   for (int64_t st : strides)
     if (st < 0 || st > INT32_MAX) return fail(CK_EUNSUPPORTED, "strides must be in [0, 2^31) elements");
   if (num_slots > INT32_MAX) return fail(CK_EUNSUPPORTED, "num_slots must be < 2^31");
@@ -112,6 +115,7 @@ extern "C" int ck_gdn_packed_decode(const void* mixed_qkv, int qkv_dtype, int64_
   p.rscale = resid_scale;
   p.out = out;
   p.idx = ssm_state_indices;
+  p.dst_idx = dst_indices;
   p.stride_mixed = (int32_t)stride_qkv_tok;
   p.stride_a = (int32_t)stride_a_tok;
   p.stride_b = (int32_t)stride_b_tok;
@@ -120,6 +124,7 @@ extern "C" int ck_gdn_packed_decode(const void* mixed_qkv, int qkv_dtype, int64_
   p.stride_resid = (int32_t)stride_resid_slot;
   p.stride_rscale = (int32_t)stride_rscale_slot;
   p.stride_idx = (int32_t)stride_indices;
+  p.stride_dst_idx = (int32_t)stride_dst_indices;
   p.num_slots = (int32_t)num_slots;
   p.scale = scale;
   const int qmax = (1 << (state_bits - 1)) - 1;
@@ -145,6 +150,58 @@ extern "C" int ck_gdn_packed_decode(const void* mixed_qkv, int qkv_dtype, int64_
     case 128: return launch_for_k<128>(p, B, resid_fmt, per_head, mode, qkv_dtype, s);
     default: return launch_for_k<256>(p, B, resid_fmt, per_head, mode, qkv_dtype, s);
   }
+}
+
+extern "C" int ck_gdn_packed_decode(const void* mixed_qkv, int qkv_dtype, int64_t stride_qkv_tok,
+                                    const void* a, int a_dtype, int64_t stride_a_tok,
+                                    const void* b, int b_dtype, int64_t stride_b_tok,
+                                    const void* A_log, int A_log_dtype,
+                                    const void* dt_bias, int dt_bias_dtype,
+                                    float scale,
+                                    int8_t* state_codes, int64_t stride_state_slot,
+                                    float* state_scale, int64_t stride_sscale_slot,
+                                    int8_t* resid_codes, int64_t stride_resid_slot,
+                                    float* resid_scale, int64_t stride_rscale_slot,
+                                    void* out, int out_dtype,
+                                    const int32_t* ssm_state_indices, int64_t stride_indices,
+                                    int64_t num_slots,
+                                    int B, int H, int HV, int K, int V,
+                                    int use_qk_l2norm, int resid_fmt, int rscale_mode,
+                                    int state_bits, int quant_mode,
+                                    void* stream) {
+  return packed_decode_impl(mixed_qkv, qkv_dtype, stride_qkv_tok, a, a_dtype, stride_a_tok, b, b_dtype, stride_b_tok,
+                            A_log, A_log_dtype, dt_bias, dt_bias_dtype, scale, state_codes, stride_state_slot,
+                            state_scale, stride_sscale_slot, resid_codes, stride_resid_slot, resid_scale,
+                            stride_rscale_slot, out, out_dtype, ssm_state_indices, stride_indices, nullptr, 0,
+                            num_slots, B, H, HV, K, V, use_qk_l2norm, resid_fmt, rscale_mode, state_bits, quant_mode,
+                            stream);
+}
+
+extern "C" int ck_gdn_packed_decode_to(const void* mixed_qkv, int qkv_dtype, int64_t stride_qkv_tok,
+                                       const void* a, int a_dtype, int64_t stride_a_tok,
+                                       const void* b, int b_dtype, int64_t stride_b_tok,
+                                       const void* A_log, int A_log_dtype,
+                                       const void* dt_bias, int dt_bias_dtype,
+                                       float scale,
+                                       int8_t* state_codes, int64_t stride_state_slot,
+                                       float* state_scale, int64_t stride_sscale_slot,
+                                       int8_t* resid_codes, int64_t stride_resid_slot,
+                                       float* resid_scale, int64_t stride_rscale_slot,
+                                       void* out, int out_dtype,
+                                       const int32_t* ssm_state_indices, int64_t stride_indices,
+                                       const int32_t* dst_state_indices, int64_t stride_dst_indices,
+                                       int64_t num_slots,
+                                       int B, int H, int HV, int K, int V,
+                                       int use_qk_l2norm, int resid_fmt, int rscale_mode,
+                                       int state_bits, int quant_mode,
+                                       void* stream) {
+  if (!dst_state_indices) return ck::fail(CK_EINVAL, "dst_state_indices is NULL (use ck_gdn_packed_decode)");
+  return packed_decode_impl(mixed_qkv, qkv_dtype, stride_qkv_tok, a, a_dtype, stride_a_tok, b, b_dtype, stride_b_tok,
+                            A_log, A_log_dtype, dt_bias, dt_bias_dtype, scale, state_codes, stride_state_slot,
+                            state_scale, stride_sscale_slot, resid_codes, stride_resid_slot, resid_scale,
+                            stride_rscale_slot, out, out_dtype, ssm_state_indices, stride_indices, dst_state_indices,
+                            stride_dst_indices, num_slots, B, H, HV, K, V, use_qk_l2norm, resid_fmt, rscale_mode,
+                            state_bits, quant_mode, stream);
 }
 
 extern "C" const char* ck_last_error(void) { return ck::last_error().c_str(); }

@@ -80,8 +80,10 @@ struct PackedParams {
   float* rscale;
   void* out;
   const int32_t* idx;
+  const int32_t* dst_idx;  // slot ids the updated state is written to (NULL: in place, to idx's slots)
   // strides in elements; validated on the host to fit in 32 bits
   int32_t stride_mixed, stride_a, stride_b, stride_state, stride_sscale, stride_resid, stride_rscale, stride_idx;
+  int32_t stride_dst_idx;
   int32_t num_slots;
   float scale;
   float qmax, rqmax;      // state code range and RN(1/qmax)
@@ -145,15 +147,20 @@ struct ItemRegs {
 
 struct ItemCoord {
   int n, hv, vt;
-  int64_t slot;
-  bool live;  // slot in [1, num_slots)
+  int64_t slot;   // slot the state is read from
+  int64_t dslot;  // slot the updated state is written to
+  bool live;      // slot in [1, num_slots)
+  bool dlive;     // dslot in [1, num_slots): the update is stored
 };
 
 // Coordinates of an item. `item` is uniform; readfirstlane keeps the results
 // in SGPRs so that the slot id is a scalar load (a vector load here would be
 // ordered behind the prefetch in the vector memory counter).
-template <bool ONE_TILE = false>  // one V-tile per (request, head): vt = 0
-__device__ __forceinline__ ItemCoord item_coord(const PackedParams& p, const int32_t* __restrict__ idx, int item) {
+// DST: the step writes to the slots in dst_idx (a second scalar load per
+// item); otherwise the destination is the source slot.
+template <bool ONE_TILE = false, bool DST = false>  // ONE_TILE: one V-tile per (request, head), vt = 0
+__device__ __forceinline__ ItemCoord item_coord(const PackedParams& p, const int32_t* __restrict__ idx,
+                                                const int32_t* __restrict__ dst_idx, int item) {
   ItemCoord ic;
   item = __builtin_amdgcn_readfirstlane(item);
   const uint32_t nh = ONE_TILE ? (uint32_t)item : fdiv((uint32_t)item, p.div_nvt);
@@ -164,6 +171,14 @@ __device__ __forceinline__ ItemCoord item_coord(const PackedParams& p, const int
   ic.vt = __builtin_amdgcn_readfirstlane(ic.vt);
   ic.slot = (int64_t)idx[(int64_t)ic.n * p.stride_idx];
   ic.live = ic.slot > 0 && ic.slot < p.num_slots;
+  if constexpr (DST) {
+    ic.dslot = (int64_t)dst_idx[(int64_t)ic.n * p.stride_dst_idx];
+    ic.dlive = ic.dslot > 0 && ic.dslot < p.num_slots;
+  } else {
+    (void)dst_idx;
+    ic.dslot = ic.slot;
+    ic.dlive = ic.live;
+  }
   return ic;
 }
 
@@ -295,7 +310,7 @@ __device__ __forceinline__ void stage_qk(const PackedParams& p, const uint32_t (
 }
 
 // Compute and store one item whose registers are loaded.
-template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ACT>
+template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ACT, bool DST>
 __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCoord& ic, int row0, int c, int lane,
                                              int wave, int parity, float alpha, float beta,
                                              const ItemRegs<RPL, Layout<K, RPL, WAVES, RESID, PER_HEAD>::EW,
@@ -328,11 +343,15 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
   const float4* q4 = reinterpret_cast<const float4*>(buf + c * 16);
   const float4* k4 = reinterpret_cast<const float4*>(buf + K + c * 16);
 
-  int8_t* sbase = p.state + ic.slot * p.stride_state + (int64_t)ic.hv * p.V * K;
-  int8_t* ebase = p.resid + ic.slot * p.stride_resid + (int64_t)ic.hv * p.V * L::RK;
-  float* scb = p.sscale + ic.slot * p.stride_sscale + (int64_t)ic.hv * p.V;
-  float* rsb = PER_HEAD ? p.rscale + ic.slot * p.stride_rscale + ic.hv
-                        : p.rscale + ic.slot * p.stride_rscale + (int64_t)ic.hv * p.V;
+  // the updated state goes to the destination slot (the source slot when the
+  // step is in place); a destination outside [1, num_slots) stores nothing
+  const bool dst_ok = DST ? ic.dlive : true;
+  const int64_t dslot = DST ? (ic.dlive ? ic.dslot : 0) : ic.slot;
+  int8_t* sbase = p.state + dslot * p.stride_state + (int64_t)ic.hv * p.V * K;
+  int8_t* ebase = p.resid + dslot * p.stride_resid + (int64_t)ic.hv * p.V * L::RK;
+  float* scb = p.sscale + dslot * p.stride_sscale + (int64_t)ic.hv * p.V;
+  float* rsb = PER_HEAD ? p.rscale + dslot * p.stride_rscale + ic.hv
+                        : p.rscale + dslot * p.stride_rscale + (int64_t)ic.hv * p.V;
   const float es_head = R.es_in[0];
 
   float ekeep[PER_HEAD && !EK_LDS ? RPL : 1][16];
@@ -412,7 +431,8 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
       const float code = quantize<MODE>(t[j], s_new, inv, yb[j]);
       t[j] = residual<MODE>(t[j], code, s_new);
     }
-    if (valid) {
+    const bool store = valid && dst_ok;
+    if (store) {
       st_stream16(sbase + (uint32_t)(r * K + c * 16),
                   u32x4{pack_low_bytes(yb[0], yb[1], yb[2], yb[3]), pack_low_bytes(yb[4], yb[5], yb[6], yb[7]),
                         pack_low_bytes(yb[8], yb[9], yb[10], yb[11]), pack_low_bytes(yb[12], yb[13], yb[14], yb[15])});
@@ -440,7 +460,7 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
       uint32_t eb[16];
 #pragma unroll
       for (int j = 0; j < 16; ++j) (void)quantize<MODE>(t[j], es, inv_e, eb[j]);
-      if (valid) {
+      if (store) {
         store_resid<RESID>(ebase + (uint32_t)(r * L::RK + c * (L::RK / LPR)), eb);
         if (c == 0) st_at<float>(rsb, (uint32_t)r * 4u, es);
       }
@@ -472,9 +492,9 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
         }
         (void)quantize<MODE>(ev, es, inv_e, eb[j]);
       }
-      if (r < p.V) store_resid<RESID>(ebase + (uint32_t)(r * L::RK + c * (L::RK / LPR)), eb);
+      if (r < p.V && dst_ok) store_resid<RESID>(ebase + (uint32_t)(r * L::RK + c * (L::RK / LPR)), eb);
     }
-    if (threadIdx.x == 0) *rsb = es;
+    if (threadIdx.x == 0 && dst_ok) *rsb = es;
   }
 }
 
@@ -484,8 +504,10 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
 // s = 0 at its start; for item k (k >= 9 reuses k = 9's slots) s = 1 + 3k when
 // the item's processing begins, 2 + 3k once all of its loads have landed,
 // 3 + 3k when its stores are issued; s = 31 holds the HW_ID register (low
-// word) and the XCC id (high word) of the CU it ran on.
-constexpr int kTlSlots = 32;
+// word) and the XCC id (high word) of the CU it ran on; s = 32 once the
+// first item's slot id is known, 33 once its loads are issued, 34 once the
+// first gates are computed.
+constexpr int kTlSlots = 40;
 constexpr int kTlMaxWorkgroups = 2048;
 
 __device__ __forceinline__ void tl_mark(const PackedParams& p, int slot) {
@@ -626,9 +648,9 @@ __device__ __forceinline__ void gates_for_items(const PackedParams& p, const Wor
 template <int RPL, int WAVES>
 constexpr int kMinWavesPerEU = (RPL == 2 && (WAVES == 8 || WAVES == 4)) ? 4 : 1;
 
-template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ACT>
+template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ACT, bool DST>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(kMinWavesPerEU<RPL, WAVES>)))
-void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx) {
+void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx, const int32_t* __restrict__ dst_idx) {
   using L = Layout<K, RPL, WAVES, RESID, PER_HEAD>;
   __shared__ __attribute__((aligned(16))) float s_qk[4][2 * K];  // [parity] staged, [2 + parity] raw
   __shared__ float s_red[2][WAVES];
@@ -650,23 +672,32 @@ void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx)
   // the barriers, so the parity follows a count of live items): two uses of
   // one buffer are always separated by the barrier of the live item between.
   ItemRegs<RPL, L::EW, L::QKT> A, B;
-  ItemCoord ca = item_coord(p, idx, item), cb;
+  ItemCoord ca = item_coord<false, DST>(p, idx, dst_idx, item), cb;
+#if CK_TIMELINE
+  asm volatile("" ::"s"((int)ca.slot));
+  tl_mark(p, 32);
+#endif
   load_item<K, RPL, WAVES, RESID, PER_HEAD, ACT>(p, ca, true, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, A);
+  tl_mark(p, 33);
   float alpha_v, beta_v;
   gates_for_items(p, w, 0, lane, alpha_v, beta_v);  // its loads overlap the first item's
+#if CK_TIMELINE
+  asm volatile("" ::"v"(alpha_v), "v"(beta_v));
+  tl_mark(p, 34);
+#endif
   int k = 0;     // item number within this workgroup
   int live = 0;  // live items processed so far
   for (;;) {
     // ---- item k in A; prefetch item k+1 into B (past the end: re-read the last item) ----
     int next = item + w.step;
-    cb = item_coord(p, idx, min(next, last));
+    cb = item_coord<false, DST>(p, idx, dst_idx, min(next, last));
     load_item<K, RPL, WAVES, RESID, PER_HEAD, ACT>(p, cb, next < item_end, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, B);
     {
       const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), k & 63));
       const float beta = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(beta_v), k & 63));
       tl_mark(p, tl_item_slot(k, 0));
       tl_data_ready(p, k, A);
-      process_item<K, RPL, WAVES, RESID, PER_HEAD, MODE, ACT>(p, ca, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c,
+      process_item<K, RPL, WAVES, RESID, PER_HEAD, MODE, ACT, DST>(p, ca, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c,
                                                           lane, wave, live & 1, alpha, beta, A, s_qk, s_red, s_ek);
       live += ca.live ? 1 : 0;
       tl_mark(p, tl_item_slot(k, 2));
@@ -678,14 +709,14 @@ void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx)
 
     // ---- item k in B; prefetch item k+1 into A ----
     next = item + w.step;
-    ca = item_coord(p, idx, min(next, last));
+    ca = item_coord<false, DST>(p, idx, dst_idx, min(next, last));
     load_item<K, RPL, WAVES, RESID, PER_HEAD, ACT>(p, ca, next < item_end, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, A);
     {
       const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), k & 63));
       const float beta = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(beta_v), k & 63));
       tl_mark(p, tl_item_slot(k, 0));
       tl_data_ready(p, k, B);
-      process_item<K, RPL, WAVES, RESID, PER_HEAD, MODE, ACT>(p, cb, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c,
+      process_item<K, RPL, WAVES, RESID, PER_HEAD, MODE, ACT, DST>(p, cb, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c,
                                                           lane, wave, live & 1, alpha, beta, B, s_qk, s_red, s_ek);
       live += cb.live ? 1 : 0;
       tl_mark(p, tl_item_slot(k, 2));
@@ -701,7 +732,7 @@ void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx)
 // device; *per_cu (if given) receives the occupancy per CU.
 int resident_workgroups(const void* fn, int block, int* per_cu = nullptr);
 
-template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ACT>
+template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ACT, bool DST>
 int launch_cfg(PackedParams p, int B, hipStream_t stream) {
   using L = Layout<K, RPL, WAVES, RESID, PER_HEAD>;
   const int nvt = PER_HEAD ? 1 : (p.V + L::ROWS_WG - 1) / L::ROWS_WG;
@@ -711,7 +742,7 @@ int launch_cfg(PackedParams p, int B, hipStream_t stream) {
   p.items = (int)items;
   p.div_nvt = make_fastdiv((uint32_t)nvt);
   p.div_hv = make_fastdiv((uint32_t)p.HV);
-  auto fn = packed_decode_kernel<K, RPL, WAVES, RESID, PER_HEAD, MODE, ACT>;
+  auto fn = packed_decode_kernel<K, RPL, WAVES, RESID, PER_HEAD, MODE, ACT, DST>;
   int per_cu = 0;
   const int resident = resident_workgroups(reinterpret_cast<const void*>(fn), WAVES * 64, &per_cu);
   if (resident <= 0) return fail(CK_ELAUNCH, "cannot query the device occupancy");
@@ -719,7 +750,7 @@ int launch_cfg(PackedParams p, int B, hipStream_t stream) {
   const int per_wg = (p.items + resident - 1) / resident;
   const int grid = (p.items + per_wg - 1) / per_wg;
   set_cu_shares(p, grid, resident, per_cu);
-  hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(WAVES * 64), 0, stream, p, p.idx);
+  hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(WAVES * 64), 0, stream, p, p.idx, p.dst_idx);
   return check_launch("ck_gdn_packed_decode");
 }
 
@@ -731,22 +762,22 @@ int launch_cfg(PackedParams p, int B, hipStream_t stream) {
 // is 8 waves of 2 rows per lane, which fits 128 VGPRs (the int8 residual's
 // unquantized values wait for the head amax in LDS) and so two workgroups per
 // CU; other K keep 4 rows per lane.
-template <int K, int RESID, bool PER_HEAD, int MODE, int ACT>
+template <int K, int RESID, bool PER_HEAD, int MODE, int ACT, bool DST>
 int launch_k(const PackedParams& p, int B, hipStream_t stream) {
   constexpr int RPI = 64 / (K / 16);
   if constexpr (!PER_HEAD) {
     if ((int64_t)B * p.HV * ((p.V + RPI * 8 - 1) / (RPI * 8)) >= 512)
-      return launch_cfg<K, 2, 4, RESID, false, MODE, ACT>(p, B, stream);
-    return launch_cfg<K, 4, 1, RESID, false, MODE, ACT>(p, B, stream);
+      return launch_cfg<K, 2, 4, RESID, false, MODE, ACT, DST>(p, B, stream);
+    return launch_cfg<K, 4, 1, RESID, false, MODE, ACT, DST>(p, B, stream);
   } else {
     const int need = p.V;
     if constexpr (K == 128) {
-      if (need > RPI * 4 * 2 && need <= RPI * 2 * 8) return launch_cfg<K, 2, 8, RESID, true, MODE, ACT>(p, B, stream);
+      if (need > RPI * 4 * 2 && need <= RPI * 2 * 8) return launch_cfg<K, 2, 8, RESID, true, MODE, ACT, DST>(p, B, stream);
     }
-    if (need <= RPI * 4 * 1) return launch_cfg<K, 4, 1, RESID, true, MODE, ACT>(p, B, stream);
-    if (need <= RPI * 4 * 2) return launch_cfg<K, 4, 2, RESID, true, MODE, ACT>(p, B, stream);
-    if (need <= RPI * 4 * 4) return launch_cfg<K, 4, 4, RESID, true, MODE, ACT>(p, B, stream);
-    if (need <= RPI * 4 * 8) return launch_cfg<K, 4, 8, RESID, true, MODE, ACT>(p, B, stream);
+    if (need <= RPI * 4 * 1) return launch_cfg<K, 4, 1, RESID, true, MODE, ACT, DST>(p, B, stream);
+    if (need <= RPI * 4 * 2) return launch_cfg<K, 4, 2, RESID, true, MODE, ACT, DST>(p, B, stream);
+    if (need <= RPI * 4 * 4) return launch_cfg<K, 4, 4, RESID, true, MODE, ACT, DST>(p, B, stream);
+    if (need <= RPI * 4 * 8) return launch_cfg<K, 4, 8, RESID, true, MODE, ACT, DST>(p, B, stream);
     return fail(CK_EUNSUPPORTED, "per-head residual scale supports V <= %d at K=%d, got V=%d", RPI * 32, K, p.V);
   }
 }
@@ -756,15 +787,22 @@ int launch_k(const PackedParams& p, int B, hipStream_t stream) {
 template <int K, int ACT>
 int launch_for_act(const PackedParams& p, int B, int resid_fmt, int per_head, int mode, hipStream_t s) {
   const bool i4 = resid_fmt == CK_RESID_INT4;
+  if (p.dst_idx) {  // out-of-place step: instantiated for the FAST arithmetic only
+    if (mode != kFast) return fail(CK_EUNSUPPORTED, "dst_state_indices needs quant_mode FAST");
+    return i4 ? (per_head ? launch_k<K, kResidInt4, true, kFast, ACT, true>(p, B, s)
+                          : launch_k<K, kResidInt4, false, kFast, ACT, true>(p, B, s))
+              : (per_head ? launch_k<K, kResidInt8, true, kFast, ACT, true>(p, B, s)
+                          : launch_k<K, kResidInt8, false, kFast, ACT, true>(p, B, s));
+  }
   if (mode == kFast)
-    return i4 ? (per_head ? launch_k<K, kResidInt4, true, kFast, ACT>(p, B, s)
-                          : launch_k<K, kResidInt4, false, kFast, ACT>(p, B, s))
-              : (per_head ? launch_k<K, kResidInt8, true, kFast, ACT>(p, B, s)
-                          : launch_k<K, kResidInt8, false, kFast, ACT>(p, B, s));
-  return i4 ? (per_head ? launch_k<K, kResidInt4, true, kExact, ACT>(p, B, s)
-                        : launch_k<K, kResidInt4, false, kExact, ACT>(p, B, s))
-            : (per_head ? launch_k<K, kResidInt8, true, kExact, ACT>(p, B, s)
-                        : launch_k<K, kResidInt8, false, kExact, ACT>(p, B, s));
+    return i4 ? (per_head ? launch_k<K, kResidInt4, true, kFast, ACT, false>(p, B, s)
+                          : launch_k<K, kResidInt4, false, kFast, ACT, false>(p, B, s))
+              : (per_head ? launch_k<K, kResidInt8, true, kFast, ACT, false>(p, B, s)
+                          : launch_k<K, kResidInt8, false, kFast, ACT, false>(p, B, s));
+  return i4 ? (per_head ? launch_k<K, kResidInt4, true, kExact, ACT, false>(p, B, s)
+                        : launch_k<K, kResidInt4, false, kExact, ACT, false>(p, B, s))
+            : (per_head ? launch_k<K, kResidInt8, true, kExact, ACT, false>(p, B, s)
+                        : launch_k<K, kResidInt8, false, kExact, ACT, false>(p, B, s));
 }
 
 template <int K>

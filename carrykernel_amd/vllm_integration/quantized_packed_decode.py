@@ -28,6 +28,11 @@ Differences from the reference, all additive:
     the correctly rounded quotient ``t / s`` with op-by-op rounding.
   * Slot ids >= num_slots make the kernel emit NaN and skip the state, where
     the reference would access memory out of bounds.
+  * ``dst_state_indices`` writes the updated state to other slots than the
+    ones read (speculative-decode chains, decoding from a shared prefix slot).
+  * ``copy_quantized_state`` / ``reset_quantized_state`` move or clear whole
+    slots (codes, scales and the EF residual together), the cache operations
+    the reference leaves to the engine (its "Stage B", CLAUDE.md:235-239).
   * Tensors must be on a GPU; there is no CPU fallback.
 """
 
@@ -97,12 +102,18 @@ def quantized_gated_delta_rule_packed_decode(
     *,
     state_bits: int = 8,
     quant_mode: str = "fast",
+    dst_state_indices: torch.Tensor | None = None,
 ):
     """INT8 + error-feedback drop-in for ``fused_recurrent_gated_delta_rule_packed_decode``.
 
     Signature of quantized_packed_decode.py:242-257. Updates the four pool
     tensors and ``out`` in place, asynchronously on the current stream, and
     returns ``out``.
+
+    ``dst_state_indices`` (int32 ``[>= B]``, optional): request n reads slot
+    ``ssm_state_indices[n]`` and writes its updated state to slot
+    ``dst_state_indices[n]`` of the same pool; an id outside
+    ``[1, num_slots)`` discards the update (``out`` is still written).
     """
     if not _native.library_available():
         raise RuntimeError("The HIP library is required for the quantized packed decode "
@@ -183,12 +194,21 @@ def quantized_gated_delta_rule_packed_decode(
         raise ValueError(f"quant_mode must be one of {tuple(_QUANT_MODES)}, got {quant_mode!r}")
     if not 2 <= int(state_bits) <= 8:
         raise ValueError(f"state_bits must be in 2..8, got {state_bits}")
+    if dst_state_indices is not None:
+        if dst_state_indices.dim() != 1 or dst_state_indices.dtype != torch.int32:
+            raise ValueError("dst_state_indices must be a 1-D int32 tensor")
+        if quant_mode != "fast":
+            raise ValueError("dst_state_indices is supported with quant_mode='fast'")
+        if dst_state_indices.shape[0] < B:
+            raise ValueError(f"dst_state_indices must have at least B={B} entries")
 
     dev = state_codes.get_device()   # -1 for a CPU tensor
     tensors = (("mixed_qkv", mixed_qkv), ("a", a), ("b", b), ("A_log", A_log),
                ("dt_bias", dt_bias), ("state_codes", state_codes), ("state_scale", state_scale),
                ("resid_codes", resid_codes), ("resid_scale", resid_scale), ("out", out),
                ("ssm_state_indices", ssm_state_indices))
+    if dst_state_indices is not None:
+        tensors += (("dst_state_indices", dst_state_indices),)
     for name, t in tensors:
         if t.get_device() != dev or dev < 0:
             _native.require_gpu(t, name)
@@ -196,27 +216,134 @@ def quantized_gated_delta_rule_packed_decode(
             raise ValueError(f"{name} is on {t.device}, the state pool on {state_codes.device}")
     if _DEBUG:
         _check_indices_host(ssm_state_indices[:B], num_slots)
+        if dst_state_indices is not None:
+            _check_dst_indices_host(ssm_state_indices[:B], dst_state_indices[:B], num_slots)
 
     L = _native.lib()
-    status = L.ck_gdn_packed_decode(
-        mixed_qkv.data_ptr(), _native.dtype_code(mixed_qkv, "mixed_qkv"), mixed_qkv.stride(0),
-        a.data_ptr(), _native.dtype_code(a, "a"), a.stride(0),
-        b.data_ptr(), _native.dtype_code(b, "b"), b.stride(0),
-        A_log.data_ptr(), _native.dtype_code(A_log, "A_log"),
-        dt_bias.data_ptr(), _native.dtype_code(dt_bias, "dt_bias"),
-        float(scale),
-        state_codes.data_ptr(), state_codes.stride(0),
-        state_scale.data_ptr(), state_scale.stride(0),
-        resid_codes.data_ptr(), resid_codes.stride(0),
-        resid_scale.data_ptr(), resid_scale.stride(0),
-        out.data_ptr(), _native.dtype_code(out, "out"),
-        ssm_state_indices.data_ptr(), ssm_state_indices.stride(0),
-        num_slots, B, H, HV, K, V,
-        int(bool(use_qk_l2norm_in_kernel)), int(resid_fmt), rscale_mode,
-        int(state_bits), _QUANT_MODES[quant_mode],
-        _native.stream_handle(dev))
+    head = (mixed_qkv.data_ptr(), _native.dtype_code(mixed_qkv, "mixed_qkv"), mixed_qkv.stride(0),
+            a.data_ptr(), _native.dtype_code(a, "a"), a.stride(0),
+            b.data_ptr(), _native.dtype_code(b, "b"), b.stride(0),
+            A_log.data_ptr(), _native.dtype_code(A_log, "A_log"),
+            dt_bias.data_ptr(), _native.dtype_code(dt_bias, "dt_bias"),
+            float(scale),
+            state_codes.data_ptr(), state_codes.stride(0),
+            state_scale.data_ptr(), state_scale.stride(0),
+            resid_codes.data_ptr(), resid_codes.stride(0),
+            resid_scale.data_ptr(), resid_scale.stride(0),
+            out.data_ptr(), _native.dtype_code(out, "out"),
+            ssm_state_indices.data_ptr(), ssm_state_indices.stride(0))
+    tail = (num_slots, B, H, HV, K, V,
+            int(bool(use_qk_l2norm_in_kernel)), int(resid_fmt), rscale_mode,
+            int(state_bits), _QUANT_MODES[quant_mode],
+            _native.stream_handle(dev))
+    if dst_state_indices is None:
+        status = L.ck_gdn_packed_decode(*head, *tail)
+    else:
+        status = L.ck_gdn_packed_decode_to(*head, dst_state_indices.data_ptr(), dst_state_indices.stride(0),
+                                           *tail)
     _native.check(status, "quantized_gated_delta_rule_packed_decode")
     return out
+
+
+def _check_dst_indices_host(src: torch.Tensor, dst: torch.Tensor, num_slots: int) -> None:
+    s = src.detach().to("cpu").tolist()
+    d = dst.detach().to("cpu").tolist()
+    live_d = [j for i, j in zip(s, d) if 0 < i < num_slots and 0 < j < num_slots]
+    if len(set(live_d)) != len(live_d):
+        raise ValueError("dst_state_indices has duplicate slot ids (the writes would race)")
+    read = {i for i in s if 0 < i < num_slots}
+    if any(j in read and j != i for i, j in zip(s, d) if 0 < i < num_slots and 0 < j < num_slots):
+        raise ValueError("a destination slot is also read by another request of the call (race)")
+
+
+def _pool_layout(pool, name: str):
+    """(HV, V, K, resid_fmt, rscale_mode) of a quantized pool tuple, validated."""
+    if len(pool) != 4:
+        raise ValueError(f"{name} must be (state_codes, state_scale, resid_codes, resid_scale)")
+    sc, ss, rc, rs = pool
+    if sc.dim() != 4 or sc.dtype != torch.int8 or rc.dtype != torch.int8:
+        raise ValueError(f"{name}: state_codes / resid_codes must be int8 [S, HV, V, K] / [S, HV, V, K or K/2]")
+    S, HV, V, K = sc.shape
+    if rc.shape == sc.shape:
+        resid_fmt = RESID_INT8
+    elif K % 2 == 0 and rc.shape == (S, HV, V, K // 2):
+        resid_fmt = RESID_INT4
+    else:
+        raise ValueError(f"{name}: resid_codes must be {(S, HV, V, K)} or {(S, HV, V, K // 2)}, "
+                         f"got {tuple(rc.shape)}")
+    if ss.dtype != torch.float32 or ss.shape != (S, HV, V):
+        raise ValueError(f"{name}: state_scale must be float32 {(S, HV, V)}")
+    if rs.dtype != torch.float32 or rs.shape not in ((S, HV, V), (S, HV)):
+        raise ValueError(f"{name}: resid_scale must be float32 {(S, HV, V)} or {(S, HV)}")
+    rscale_mode = _native.RSCALE_PER_HEAD if rs.dim() == 2 else _native.RSCALE_PER_ROW
+    for tname, t in zip(("state_codes", "state_scale", "resid_codes", "resid_scale"), pool):
+        if not _slot_contiguous(t):
+            raise ValueError(f"{name}: {tname} must be contiguous within a slot")
+    return HV, V, K, resid_fmt, rscale_mode
+
+
+def _require_pool_gpu(pool, name: str):
+    for tname, t in zip(("state_codes", "state_scale", "resid_codes", "resid_scale"), pool):
+        _native.require_gpu(t, f"{name}.{tname}")
+        if t.device != pool[0].device:
+            raise ValueError(f"{name}: {tname} is on {t.device}, state_codes on {pool[0].device}")
+
+
+def _pool_args(pool):
+    sc, ss, rc, rs = pool
+    return (sc.data_ptr(), sc.stride(0), ss.data_ptr(), ss.stride(0), rc.data_ptr(), rc.stride(0),
+            rs.data_ptr(), rs.stride(0), sc.shape[0])
+
+
+def _slot_ids(ids: torch.Tensor, name: str, device) -> torch.Tensor:
+    if ids.dim() != 1 or ids.dtype != torch.int32:
+        raise ValueError(f"{name} must be a 1-D int32 tensor")
+    if ids.device != device:
+        raise ValueError(f"{name} is on {ids.device}, the pool on {device}")
+    return ids.contiguous()
+
+
+def copy_quantized_state(src_pool, src_ids: torch.Tensor, dst_pool, dst_ids: torch.Tensor):
+    """Copy whole slots between quantized pools of the same layout: slot
+    ``src_ids[i]`` of ``src_pool`` -> slot ``dst_ids[i]`` of ``dst_pool``, state
+    codes and scales together with the error-feedback residual and its
+    scales (prefix-cache fork, speculative-decode checkpoint, moving a
+    preempted request's state to and from a staging pool). Pools are the
+    4-tuples ``init_quantized_state`` returns and may be the same; a slot must
+    not be both read and written by one call. Ids outside ``[1, S)`` of their
+    pool skip the pair. Asynchronous on the current stream."""
+    layout = _pool_layout(src_pool, "src_pool")
+    if _pool_layout(dst_pool, "dst_pool") != layout:
+        raise ValueError("src_pool and dst_pool must have the same HV, V, K, residual format and scale layout")
+    _require_pool_gpu(src_pool, "src_pool")
+    _require_pool_gpu(dst_pool, "dst_pool")
+    dev = src_pool[0].device
+    if dst_pool[0].device != dev:
+        raise ValueError("src_pool and dst_pool must be on the same GPU")
+    src_ids = _slot_ids(src_ids, "src_ids", dev)
+    dst_ids = _slot_ids(dst_ids, "dst_ids", dev)
+    if src_ids.shape != dst_ids.shape:
+        raise ValueError("src_ids and dst_ids must have the same length")
+    HV, V, K, resid_fmt, rscale_mode = layout
+    status = _native.lib().ck_pool_copy_slots(
+        *_pool_args(src_pool), *_pool_args(dst_pool), src_ids.data_ptr(), dst_ids.data_ptr(), src_ids.shape[0],
+        HV, V, K, resid_fmt, rscale_mode, _native.stream_handle(dev))
+    _native.check(status, "copy_quantized_state")
+
+
+def reset_quantized_state(pool, ids: torch.Tensor):
+    """Zero the listed slots (codes, scales, residual and residual scales):
+    the state of a new request, as ``init_quantized_state`` without ``h0``
+    gives (quantized_packed_decode.py:341-345). Ids outside ``[1, S)`` are
+    skipped. Asynchronous on the current stream."""
+    HV, V, K, resid_fmt, rscale_mode = _pool_layout(pool, "pool")
+    _require_pool_gpu(pool, "pool")
+    dev = pool[0].device
+    ids = _slot_ids(ids, "ids", dev)
+    status = _native.lib().ck_pool_reset_slots(
+        *_pool_args(pool), ids.data_ptr(), ids.shape[0], HV, V, K, resid_fmt, rscale_mode,
+        _native.stream_handle(dev))
+    _native.check(status, "reset_quantized_state")
 
 
 def init_quantized_state(num_slots: int, HV: int, V: int, K: int, device,

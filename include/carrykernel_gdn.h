@@ -25,6 +25,14 @@
  *   ck_hbm_copy               <- measurement only: the device-to-device copy that
  *                                experiments/cuda_bench.py:39-60 times as the
  *                                measured bandwidth peak
+ *   ck_gdn_packed_decode_to   <- the same step as ck_gdn_packed_decode with the
+ *   ck_pool_copy_slots           updated state written to other slots, and slot
+ *   ck_pool_reset_slots          copy / reset of the pool: the engine-side cache
+ *                                operations the reference leaves open (its "Stage B":
+ *                                the EF residual must move with the state through
+ *                                paging, preemption, prefix-cache reuse and
+ *                                speculative-decode rollback, CLAUDE.md:235-239,
+ *                                266-273); no reference code implements them
  */
 #ifndef CARRYKERNEL_GDN_H_
 #define CARRYKERNEL_GDN_H_
@@ -107,6 +115,67 @@ int ck_gdn_packed_decode(const void* mixed_qkv, int qkv_dtype, int64_t stride_qk
                          int use_qk_l2norm, int resid_fmt, int rscale_mode,
                          int state_bits, int quant_mode,
                          void* stream);
+
+/*
+ * ck_gdn_packed_decode with the updated state written to the slots in
+ * dst_state_indices [B] (int32, stride in elements) instead of back to the
+ * slots it was read from: request n reads slot ssm_state_indices[n] and
+ * writes slot dst_state_indices[n] of the same pool (the two may be equal).
+ * A destination id outside [1, num_slots) discards the update (out is still
+ * written). Reading a slot that another request of the same call writes is a
+ * race. Chains of calls (token t reads the slot token t-1 wrote) keep every
+ * intermediate state, which is what speculative decoding needs to roll back;
+ * a shared prefix slot can be decoded into a request's own slot without a
+ * copy. dst_state_indices must not be NULL; quant_mode must be CK_QUANT_FAST
+ * (other modes return CK_EUNSUPPORTED).
+ */
+int ck_gdn_packed_decode_to(const void* mixed_qkv, int qkv_dtype, int64_t stride_qkv_tok,
+                            const void* a, int a_dtype, int64_t stride_a_tok,
+                            const void* b, int b_dtype, int64_t stride_b_tok,
+                            const void* A_log, int A_log_dtype,
+                            const void* dt_bias, int dt_bias_dtype,
+                            float scale,
+                            int8_t* state_codes, int64_t stride_state_slot,
+                            float* state_scale, int64_t stride_sscale_slot,
+                            int8_t* resid_codes, int64_t stride_resid_slot,
+                            float* resid_scale, int64_t stride_rscale_slot,
+                            void* out, int out_dtype,
+                            const int32_t* ssm_state_indices, int64_t stride_indices,
+                            const int32_t* dst_state_indices, int64_t stride_dst_indices,
+                            int64_t num_slots,
+                            int B, int H, int HV, int K, int V,
+                            int use_qk_l2norm, int resid_fmt, int rscale_mode,
+                            int state_bits, int quant_mode,
+                            void* stream);
+
+/*
+ * Copy n slots between quantized pools of the same layout (HV, V, K,
+ * resid_fmt, rscale_mode; the vLLM layout of ck_gdn_packed_decode): slot
+ * src_ids[i] of the source pool -> slot dst_ids[i] of the destination pool,
+ * all four regions (state codes and scales, residual codes and scales). The
+ * pools may be the same tensors; a slot must not be both read and written by
+ * one call. Pairs with an id outside [1, num_slots) of its pool are skipped.
+ * Each slot's region must be contiguous; slot strides are in elements of the
+ * region's type. n <= 65535. Device memory only.
+ */
+int ck_pool_copy_slots(const int8_t* src_state, int64_t src_stride_state, const float* src_sscale,
+                       int64_t src_stride_sscale, const int8_t* src_resid, int64_t src_stride_resid,
+                       const float* src_rscale, int64_t src_stride_rscale, int64_t src_num_slots,
+                       int8_t* dst_state, int64_t dst_stride_state, float* dst_sscale,
+                       int64_t dst_stride_sscale, int8_t* dst_resid, int64_t dst_stride_resid,
+                       float* dst_rscale, int64_t dst_stride_rscale, int64_t dst_num_slots,
+                       const int32_t* src_ids, const int32_t* dst_ids, int n,
+                       int HV, int V, int K, int resid_fmt, int rscale_mode, void* stream);
+
+/*
+ * Zero the four regions of the n slots ids[i] (ids outside [1, num_slots) are
+ * skipped): the state of a new request, as init_quantized_state without h0
+ * gives (vllm_integration/quantized_packed_decode.py:341-345).
+ */
+int ck_pool_reset_slots(int8_t* state, int64_t stride_state, float* sscale, int64_t stride_sscale,
+                        int8_t* resid, int64_t stride_resid, float* rscale, int64_t stride_rscale,
+                        int64_t num_slots, const int32_t* ids, int n,
+                        int HV, int V, int K, int resid_fmt, int rscale_mode, void* stream);
 
 /*
  * Same step with an unquantized state pool (fp32 or bf16), the layout and

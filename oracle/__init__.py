@@ -61,7 +61,7 @@ def lib():
             L.orc_packed_decode.argtypes = [
                 _f32p, _i64, _f32p, _i64, _f32p, _i64, _f32p, _f32p, _flt,
                 _i8p, _i64, _f32p, _i64, _i8p, _i64, _f32p, _i64,
-                _f32p, _i32p, _i64,
+                _f32p, _i32p, ctypes.c_void_p, _i64,
                 _int, _int, _int, _int, _int,
                 _int, _int, _int, _int, _int, _int]
             L.orc_quantize_rows.argtypes = [_f32p, _i64, _int, _flt, _i8p, _f32p]
@@ -129,13 +129,16 @@ def gates(a, b, A_log, dt_bias):
 def packed_decode(mixed_qkv, a, b, A_log, dt_bias, scale,
                   state_codes, state_scale, resid_codes, resid_scale,
                   indices, H, *, use_qk_l2norm=False, resid_fmt=RESID_INT8,
-                  per_head=False, state_bits=8, mode=MODE_FAST, nthreads=0):
+                  per_head=False, state_bits=8, mode=MODE_FAST, nthreads=0, dst_indices=None):
     """One step of quantized_packed_decode.py:116-239 on host arrays.
 
     The pool arrays (``state_codes [S,HV,V,K]`` int8, ``state_scale [S,HV,V]``,
     ``resid_codes [S,HV,V,K or K/2]`` int8, ``resid_scale [S,HV,V]`` or
     ``[S,HV]`` when ``per_head``) are updated in place and must be
     C-contiguous numpy arrays. Returns ``out [B, HV, V]`` fp32.
+    ``dst_indices`` (optional): request n's updated state goes to slot
+    ``dst_indices[n]`` (outside ``[1, S)``: discarded) instead of the slot
+    it was read from.
     """
     mixed = _f32(mixed_qkv)
     a = _f32(a)
@@ -150,11 +153,12 @@ def packed_decode(mixed_qkv, a, b, A_log, dt_bias, scale,
     S, HV, V, K = state_codes.shape
     B = mixed.shape[0]
     out = np.empty((B, HV, V), dtype=np.float32)
+    didx = None if dst_indices is None else np.ascontiguousarray(np.asarray(dst_indices, dtype=np.int32))
     rc = lib().orc_packed_decode(
         mixed, mixed.shape[1], a, a.shape[1], b, b.shape[1], A_log, dt_bias, float(scale),
         state_codes, state_codes[0].size, state_scale, state_scale[0].size,
         resid_codes, resid_codes[0].size, resid_scale, resid_scale[0].size,
-        out, idx, S, B, H, HV, K, V,
+        out, idx, None if didx is None else didx.ctypes.data_as(ctypes.c_void_p), S, B, H, HV, K, V,
         int(bool(use_qk_l2norm)), int(resid_fmt), int(bool(per_head)), int(state_bits),
         int(mode), int(nthreads))
     if rc != 0:

@@ -205,9 +205,11 @@ int orc_packed_decode(const float* mixed, int64_t stride_mixed,
                       const float* A_log, const float* dt_bias, float scale,
                       int8_t* state, int64_t stride_state, float* sscale, int64_t stride_sscale,
                       int8_t* resid, int64_t stride_resid, float* rscale, int64_t stride_rscale,
-                      float* out, const int32_t* idx, int64_t num_slots,
+                      float* out, const int32_t* idx, const int32_t* dst_idx, int64_t num_slots,
                       int B, int H, int HV, int K, int V,
                       int l2norm, int resid_fmt, int per_head, int state_bits, int mode, int nthreads) {
+  /* dst_idx (may be NULL: in place): the updated state of request n goes to
+     slot dst_idx[n]; one outside [1, num_slots) discards it (out is kept). */
   if (K % 16 != 0 || K > 256 || (K / 16 & (K / 16 - 1)) != 0 || HV % H != 0) return 1;
   const float qmax = (float)((1 << (state_bits - 1)) - 1);
   const float qmax_e = resid_fmt == 1 ? 7.0f : 127.0f;
@@ -255,17 +257,26 @@ int orc_packed_decode(const float* mixed, int64_t stride_mixed,
       float alpha, beta;
       orc_gates(a[(int64_t)n * stride_a + hv], b[(int64_t)n * stride_b + hv], A_log[hv], dt_bias[hv], &alpha, &beta);
 
-      int8_t* st = state + slot * stride_state + (int64_t)hv * V * K;
-      float* ss = sscale + slot * stride_sscale + (int64_t)hv * V;
-      int8_t* er = resid + slot * stride_resid + (int64_t)hv * V * RK;
-      float* rs = per_head ? rscale + slot * stride_rscale + hv : rscale + slot * stride_rscale + (int64_t)hv * V;
+      const int64_t dslot = dst_idx ? (int64_t)dst_idx[n] : slot;
+      const int store = dslot > 0 && dslot < num_slots;
+      const int8_t* st = state + slot * stride_state + (int64_t)hv * V * K;
+      const float* ss = sscale + slot * stride_sscale + (int64_t)hv * V;
+      const int8_t* er = resid + slot * stride_resid + (int64_t)hv * V * RK;
+      const float* rs = per_head ? rscale + slot * stride_rscale + hv : rscale + slot * stride_rscale + (int64_t)hv * V;
+      const int64_t ws = store ? dslot : slot; /* write targets (used only when store) */
+      int8_t* st_w = state + ws * stride_state + (int64_t)hv * V * K;
+      float* ss_w = sscale + ws * stride_sscale + (int64_t)hv * V;
+      int8_t* er_w = resid + ws * stride_resid + (int64_t)hv * V * RK;
+      float* rs_w = per_head ? rscale + ws * stride_rscale + hv : rscale + ws * stride_rscale + (int64_t)hv * V;
       const float* vv = m + 2 * (int64_t)H * K + (int64_t)hv * V;
       const float rs_head = per_head ? rs[0] : 0.0f;
       float ea_head = 0.0f;
 
       for (int r = 0; r < V; ++r) {
-        int8_t* crow = st + (int64_t)r * K;
-        int8_t* erow = er + (int64_t)r * RK;
+        const int8_t* crow = st + (int64_t)r * K;
+        const int8_t* erow = er + (int64_t)r * RK;
+        int8_t* crow_w = st_w + (int64_t)r * K;
+        int8_t* erow_w = er_w + (int64_t)r * RK;
         /* dequantize + decay (qpd:158, :185) */
         if (mode == MODE_FAST) {
           const float sa = ss[r] * alpha;
@@ -292,10 +303,10 @@ int orc_packed_decode(const float* mixed, int64_t stride_mixed,
         float* e = ebuf + (int64_t)r * K;
         for (int j = 0; j < K; ++j) {
           const float c = quant_code(h[j], s_new, inv, qmax, mode);
-          crow[j] = (int8_t)c;
+          if (store) crow_w[j] = (int8_t)c;
           e[j] = resid_of(h[j], c, s_new, mode);
         }
-        ss[r] = s_new;
+        if (store) ss_w[r] = s_new;
         if (per_head) {
           for (int j = 0; j < K; ++j) ea_head = fmaxf(ea_head, fabsf(e[j]));
         } else { /* residual quantize, per V-row scale (qpd:211-215) */
@@ -304,28 +315,30 @@ int orc_packed_decode(const float* mixed, int64_t stride_mixed,
           const float es = fmaxf(ea / qmax_e, ORC_EPS);
           const float inv_e = 1.0f / es;
           for (int j = 0; j < K; ++j) codes[j] = (int)quant_code(e[j], es, inv_e, qmax_e, mode);
-          if (resid_fmt == 1) {
-            pack_i4_row(erow, codes, K);
-          } else {
-            for (int j = 0; j < K; ++j) erow[j] = (int8_t)codes[j];
+          if (store) {
+            if (resid_fmt == 1) {
+              pack_i4_row(erow_w, codes, K);
+            } else {
+              for (int j = 0; j < K; ++j) erow_w[j] = (int8_t)codes[j];
+            }
+            rs_w[r] = es;
           }
-          rs[r] = es;
         }
       }
-      if (per_head) { /* one residual scale per (slot, head) */
+      if (per_head && store) { /* one residual scale per (slot, head) */
         const float es = fmaxf(ea_head / qmax_e, ORC_EPS);
         const float inv_e = 1.0f / es;
         for (int r = 0; r < V; ++r) {
           const float* e = ebuf + (int64_t)r * K;
-          int8_t* erow = er + (int64_t)r * RK;
+          int8_t* erow_w = er_w + (int64_t)r * RK;
           for (int j = 0; j < K; ++j) codes[j] = (int)quant_code(e[j], es, inv_e, qmax_e, mode);
           if (resid_fmt == 1) {
-            pack_i4_row(erow, codes, K);
+            pack_i4_row(erow_w, codes, K);
           } else {
-            for (int j = 0; j < K; ++j) erow[j] = (int8_t)codes[j];
+            for (int j = 0; j < K; ++j) erow_w[j] = (int8_t)codes[j];
           }
         }
-        rs[0] = es;
+        rs_w[0] = es;
       }
     }
     free(q);
