@@ -508,7 +508,7 @@ def timeline_report(device, B, resid_fmt, per_head, groups, launches=20):
     for t in range(200):
         step(t)
     torch.cuda.synchronize()
-    slots, max_wg = 32, 2048
+    slots, max_wg = 40, 2048
     buf = torch.zeros(max_wg * slots, dtype=torch.int64, device=device)
     _native.check(L.ck_timeline_set(buf.data_ptr()), "ck_timeline_set")
     for t in range(launches - 1):
@@ -522,6 +522,8 @@ def timeline_report(device, B, resid_fmt, per_head, groups, launches=20):
     t = ts[:nwg, :31].astype(np.int64)
     t0 = t[:, 0].min()
     rel = np.where(t > 0, (t - t0) * 1e-2, np.nan)          # us
+    su = ts[:nwg, 32:35].astype(np.int64)
+    start = np.where(su > 0, (su - t0) * 1e-2, np.nan)       # slot id known, item 0 issued, gates done
     hw = (ts[:nwg, 31] & 0xffffffff).astype(np.int64)
     xcc = (ts[:nwg, 31] >> 32).astype(np.int64) & 0xf
     cu_id = xcc * 1024 + ((hw >> 13) & 7) * 64 + ((hw >> 12) & 1) * 16 + ((hw >> 8) & 0xf)
@@ -539,6 +541,10 @@ def timeline_report(device, B, resid_fmt, per_head, groups, launches=20):
     for a in range(per_cu):
         sel = slice(a * m, (a + 1) * m)
         ages.append({"age": a, "items_median": float(np.median(n_rec[sel])),
+                     "start_us": round(float(np.median(rel[sel, 0])), 2),
+                     "slot_id_known_us": round(float(np.nanmedian(start[sel, 0])), 2),
+                     "item0_loads_issued_us": round(float(np.nanmedian(start[sel, 1])), 2),
+                     "gates_done_us": round(float(np.nanmedian(start[sel, 2])), 2),
                      "first_data_us": round(float(np.median(data[sel, 0])), 2),
                      "compute_us_per_item": round(float(np.median(comp[sel])), 2),
                      "wait_us_per_item": round(float(np.median(wait[sel])), 2),

@@ -36,6 +36,41 @@ __device__ __forceinline__ float load_act(const void* p, int64_t i, int dtype) {
   return (float)static_cast<const _Float16*>(p)[i];
 }
 
+// Element i of a tensor of runtime dtype as one 4-byte load (for a 16-bit
+// element: the aligned dword that holds it, which lies inside any
+// allocation, 4-byte aligned and 4-byte granular), decoded after the load.
+// No conversion sits next to a load, so the compiler need not wait for a
+// load (and every load issued before it) until the value is decoded, and
+// several such loads can be in flight before the first is needed.
+struct ActBits {
+  uint32_t word;
+  uint32_t hi;  // 16-bit element in the high half of the word
+};
+
+__device__ __forceinline__ ActBits load_act_bits(const void* p, int64_t i, int dtype) {
+  ActBits r;
+  if (dtype == kF32) {
+    r.word = static_cast<const uint32_t*>(p)[i];
+    r.hi = 0;
+  } else {
+    const char* e = static_cast<const char*>(p) + 2 * i;
+    const uint32_t mis = (uint32_t)reinterpret_cast<uintptr_t>(e) & 3u;  // 0 or 2
+    r.word = *reinterpret_cast<const uint32_t*>(e - mis);  // pointer arithmetic keeps the global address space
+    r.hi = mis >> 1;
+  }
+  return r;
+}
+
+__device__ __forceinline__ float decode_act_bits(ActBits b, int dtype) {
+  if (dtype == kF32) return __uint_as_float(b.word);
+  const uint32_t h16 = b.hi ? (b.word >> 16) : (b.word & 0xffffu);
+  if (dtype == kBF16) return __uint_as_float(h16 << 16);
+  _Float16 h;
+  const uint16_t r16 = (uint16_t)h16;
+  __builtin_memcpy(&h, &r16, 2);
+  return (float)h;
+}
+
 // Raw bits of one activation of ESZ bytes (4: fp32, 2: bf16 / fp16) at a
 // uniform base plus a 32-bit byte offset. Conversion is deferred to
 // act_decode so that issuing the load never waits for its data.

@@ -637,9 +637,14 @@ __device__ __forceinline__ void gates_for_items(const PackedParams& p, const Wor
   const uint32_t nh = fdiv((uint32_t)item, p.div_nvt);
   const uint32_t n = fdiv(nh, p.div_hv);
   const int hv = (int)(nh - n * p.div_hv.d);
-  ck_gates(load_act(p.a, (int64_t)n * p.stride_a + hv, p.a_dtype()),
-           load_act(p.b, (int64_t)n * p.stride_b + hv, p.b_dtype()), load_act(p.A_log, hv, p.A_log_dtype()),
-           load_act(p.dt_bias, hv, p.dt_bias_dtype()), &alpha_v, &beta_v);
+  // all four loads are issued before any value is decoded: a conversion next
+  // to its load would wait for every load in flight (including the items')
+  const ActBits ra = load_act_bits(p.a, (int64_t)n * p.stride_a + hv, p.a_dtype());
+  const ActBits rb = load_act_bits(p.b, (int64_t)n * p.stride_b + hv, p.b_dtype());
+  const ActBits rA = load_act_bits(p.A_log, hv, p.A_log_dtype());
+  const ActBits rd = load_act_bits(p.dt_bias, hv, p.dt_bias_dtype());
+  ck_gates(decode_act_bits(ra, p.a_dtype()), decode_act_bits(rb, p.b_dtype()), decode_act_bits(rA, p.A_log_dtype()),
+           decode_act_bits(rd, p.dt_bias_dtype()), &alpha_v, &beta_v);
 }
 
 // Waves per SIMD the register allocation must allow: two 8-wave or four
