@@ -195,6 +195,11 @@ def test_dst_indices_front_end_errors():
                                                      resid_codes=pool[2], resid_scale=pool[3], out=out,
                                                      ssm_state_indices=idx, resid_fmt=qpd.RESID_INT4,
                                                      dst_state_indices=idx[:1])
+    with pytest.raises(ValueError, match="quant_mode='fast'"):
+        qpd.quantized_gated_delta_rule_packed_decode(**c, state_codes=pool[0], state_scale=pool[1],
+                                                     resid_codes=pool[2], resid_scale=pool[3], out=out,
+                                                     ssm_state_indices=idx, resid_fmt=qpd.RESID_INT4,
+                                                     quant_mode="exact", dst_state_indices=idx)
     qpd._check_dst_indices_host(idx, torch.tensor([1, 2], dtype=torch.int32), 4)
     with pytest.raises(ValueError, match="duplicate"):
         qpd._check_dst_indices_host(idx, torch.tensor([3, 3], dtype=torch.int32), 4)
