@@ -256,6 +256,49 @@ def _graph_time(device, step, n_steps, warmup, reps_cap=None):
     return sorted(trials)[1]
 
 
+def multilayer_token(device, layers=24, B=64, live=None, tokens=20, seed=7):
+    """Config C5's decode shape as a serving engine runs it: one token through
+    `layers` GDN layers at batch B (int4 residual, per-head scale), each layer
+    with its own pool, called eagerly (host-inclusive time per token: one
+    Python call and one launch per layer) and captured once in a HIP graph and
+    replayed (device time per token). With live < B the batch is padded with
+    NULL-block ids, as a capture at a fixed batch size is
+    (quantized_packed_decode.py:24-26,132-136); bytes count live requests."""
+    live = B if live is None else live
+    S = B + 1
+    pools = [qpd.init_quantized_state(S, HV, V, K, device, resid_fmt=qpd.RESID_INT4, per_head_resid_scale=True)
+             for _ in range(layers)]
+    sets, A_log, dt_bias = make_step_inputs(B, 1, device, seed)
+    mixed, a, b = sets[0]
+    idx = torch.arange(1, B + 1, dtype=torch.int32, device=device)
+    idx[live:] = 0
+    outs = [torch.empty(B, 1, HV, V, device=device) for _ in range(layers)]
+
+    def token(_t=0):
+        for layer in range(layers):
+            qpd.quantized_gated_delta_rule_packed_decode(mixed, a, b, A_log, dt_bias, 1.0, *pools[layer],
+                                                         outs[layer], idx, resid_fmt=qpd.RESID_INT4)
+
+    for _ in range(3):
+        token()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(tokens):
+        token()
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) * 1e3 / tokens
+    graph_ms = _graph_time(device, token, 1, 3, max(3, tokens))
+    nb = layers * algorithmic_bytes(live, H, HV, K, V, qpd.RESID_INT4, True)
+    del pools, outs
+    torch.cuda.empty_cache()
+    return {"layers": layers, "batch": B, "live_requests": live,
+            "eager_host_us_per_token": round(eager_ms * 1e3, 2),
+            "graph_us_per_token": round(graph_ms * 1e3, 2),
+            "graph_us_per_layer": round(graph_ms * 1e3 / layers, 3),
+            "GBps": round(nb / (graph_ms * 1e-3) / 1e9, 1),
+            "frac": round(nb / (graph_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+
+
 def statequant_bytes(B, HV, K, V, res_fmt):
     """Unique bytes of one statequant-layout step (statequant/kernel.py:379-408):
     int8 codes in/out, residual in/out, per-column state scale in/out (and the
@@ -686,6 +729,10 @@ def main():
                                           "frac": round(nb / (m * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
     line["sweep"] = dict(sorted(sweep.items(), key=lambda kv: (int(kv[0][1:kv[0].index("_")]), kv[0])))
     if not args.no_sweep:
+        # the C5 shape through 24 layers per token: eager vs one graph per token,
+        # full and NULL-padded (48 live requests in a batch-64 capture)
+        line["multilayer_c5"] = {"full": multilayer_token(device),
+                                 "padded": multilayer_token(device, live=48)}
         line["arms"] = arms(device)
         # measured copy ceiling at the headline's byte count and for a 1 GiB copy
         at = hbm_copy_peak(device, nbytes)
