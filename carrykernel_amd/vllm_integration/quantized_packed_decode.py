@@ -76,11 +76,20 @@ def _check_indices_host(ssm_state_indices: torch.Tensor, num_slots: int) -> None
 
 def _slot_contiguous(t: torch.Tensor) -> bool:
     """Every dim but the slot dim is densely packed (row-major)."""
+    sh, st = t.shape, t.stride()
+    n = len(sh)
+    # the usual dense layouts, without the general loop (this runs per call)
+    if n == 4 and st[3] == 1 and st[2] == sh[3] and st[1] == sh[2] * sh[3]:
+        return True
+    if n == 3 and st[2] == 1 and st[1] == sh[2]:
+        return True
+    if n == 2 and st[1] == 1:
+        return True
     expect = 1
-    for size, stride in zip(reversed(t.shape[1:]), reversed(t.stride()[1:])):
-        if size != 1 and stride != expect:
+    for i in range(n - 1, 0, -1):
+        if sh[i] != 1 and st[i] != expect:
             return False
-        expect *= size
+        expect *= sh[i]
     return True
 
 

@@ -218,3 +218,33 @@ def test_build_flags():
     flags = " ".join(build.HIPCC_FLAGS)
     assert "--offload-arch=gfx950" in flags
     assert "-packed-fp32-ops" in flags and "-ffp-contract=off" in flags
+
+
+def test_slot_contiguity_check_matches_its_definition():
+    """The per-call check (dense fast paths, general loop otherwise) against a
+    restatement of the rule: every dim after the slot dim is row-major dense,
+    size-1 dims may have any stride."""
+    def rule(t):
+        expect = 1
+        for size, stride in zip(reversed(t.shape[1:]), reversed(t.stride()[1:])):
+            if size != 1 and stride != expect:
+                return False
+            expect *= size
+        return True
+
+    g = torch.Generator().manual_seed(0)
+    cases = []
+    for shape in [(5, 4, 3, 8), (5, 1, 3, 8), (5, 4, 1, 8), (5, 4, 3, 1), (3, 6, 7), (3, 1, 7), (4, 9), (4, 1)]:
+        base = torch.empty(shape)
+        cases += [base, base[:, ...]]
+        back = torch.empty((shape[0], base[0].numel() + 5))       # padded slots (a view per slot row)
+        cases.append(back[:, :base[0].numel()].view(shape))
+        if len(shape) >= 3:
+            cases.append(base.transpose(-1, -2))                    # not row-major inside a slot
+            cases.append(torch.empty(shape[:-1] + (shape[-1] * 2,))[..., ::2])  # strided last dim
+    for _ in range(40):                                             # random size-1 dims with odd strides
+        shape = tuple(int(x) for x in torch.randint(1, 4, (4,), generator=g))
+        strides = tuple(int(x) for x in torch.randint(1, 50, (4,), generator=g))
+        cases.append(torch.empty(1000).as_strided(shape, strides))
+    for t in cases:
+        assert qpd._slot_contiguous(t) == rule(t), (tuple(t.shape), t.stride())
