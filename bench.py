@@ -287,7 +287,7 @@ def multilayer_token(device, layers=24, B=64, live=None, tokens=20, seed=7):
         token()
     torch.cuda.synchronize()
     eager_ms = (time.perf_counter() - t0) * 1e3 / tokens
-    graph_ms = _graph_time(device, token, 1, 3, max(3, tokens))
+    graph_ms = _graph_time(device, token, 1, 10, max(3, tokens))
     nb = layers * algorithmic_bytes(live, H, HV, K, V, qpd.RESID_INT4, True)
     del pools, outs
     torch.cuda.empty_cache()
@@ -309,7 +309,7 @@ def statequant_bytes(B, HV, K, V, res_fmt):
     return B * HV * per
 
 
-def arms(device, batches=(8, 64), steps=200):
+def arms(device, batches=(8, 64), steps=800):
     """The other entry points at config shapes (HV=32, K=V=128, fp32
     activations): the statequant-layout step for each residual format, its fp32
     baseline, and the unquantized fp32 / bf16 state arms of the vLLM-layout
@@ -351,7 +351,7 @@ def arms(device, batches=(8, 64), steps=200):
                                          b_[3].data_ptr(), B, HV, K, V, 127.0, res_fmt, 0,
                                          _native.stream_handle(device))
                 _native.check(st, "statequant step")
-            ms = _graph_time(device, step, nsets, 3, max(2, steps // nsets))
+            ms = _graph_time(device, step, nsets, -(-200 // nsets), max(2, steps // nsets))
             rec(f"statequant_B{B}_{sq.residual_label(res_fmt)}", ms, statequant_bytes(B, HV, K, V, res_fmt))
             del sets
         # fp32 baseline step, ping-pong between state buffers
@@ -363,7 +363,7 @@ def arms(device, batches=(8, 64), steps=200):
                                     al.data_ptr(), be.data_ptr(), o.data_ptr(), hsets[(t + 1) % nsets].data_ptr(),
                                     B, HV, K, V, _native.stream_handle(device))
             _native.check(st, "fp32 step")
-        ms = _graph_time(device, fstep, nsets, 3, max(2, steps // nsets))
+        ms = _graph_time(device, fstep, nsets, -(-200 // nsets), max(2, steps // nsets))
         rec(f"fp32_step_B{B}", ms, B * HV * (2 * 4 * K * V + 2 * 4 * K + 2 * 4 * V + 8))
         del hsets
         torch.cuda.empty_cache()
@@ -385,7 +385,7 @@ def arms(device, batches=(8, 64), steps=200):
                 0 if dtype == torch.float32 else 1, state.stride(0), out.data_ptr(), 0,
                 idxs[t % len(idxs)].data_ptr(), 1, S, B, H, HV, K, V, 0, _native.stream_handle(device))
             _native.check(st, "float-state step")
-        ms = _graph_time(device, vstep, groups, 3, max(2, steps // groups))
+        ms = _graph_time(device, vstep, groups, -(-200 // groups), max(2, steps // groups))
         rec(f"vllm_{name}_state_B{B}", ms, float_state_bytes(B, H, HV, K, V, esz))
         del state
         torch.cuda.empty_cache()
@@ -426,7 +426,7 @@ def hbm_copy_peak(device, total_bytes, pool_bytes=1 << 31, grids=(512, 2048, 409
         def step(t, grid=grid):
             _native.check(L.ck_hbm_copy(src[t % groups].data_ptr(), dst[t % groups].data_ptr(), half, grid,
                                         _native.stream_handle(device)), "hbm copy")
-        ms = _graph_time(device, step, groups, 3)
+        ms = _graph_time(device, step, groups, -(-200 // groups))
         if best is None or ms < best[0]:
             best = (ms, grid)
     if not all(bool((d[:4096] == t + 1).all()) for t, d in enumerate(dst)):
@@ -576,6 +576,9 @@ def timeline_report(device, B, resid_fmt, per_head, groups, launches=20):
     last_end = np.array([end[i, n_rec[i] - 1] for i in range(nwg)])
     comp = np.nansum(end - data, axis=1) / n_rec
     wait = np.nansum(data - begin, axis=1) / n_rec
+    # from one item's stores to the next item's start: the loop's bookkeeping, the
+    # slot-id load of the item after next and the issue of its prefetch
+    gap = np.nanmedian(begin[:, 1:] - end[:, :-1], axis=1)
     m = nwg // per_cu
     # do the workgroups q, q + m, ... share a CU (for every q)?
     groups_ok = sum(1 for q in range(m) if len({int(cu_id[q + a * m]) for a in range(per_cu)}) == 1
@@ -591,6 +594,7 @@ def timeline_report(device, B, resid_fmt, per_head, groups, launches=20):
                      "first_data_us": round(float(np.median(data[sel, 0])), 2),
                      "compute_us_per_item": round(float(np.median(comp[sel])), 2),
                      "wait_us_per_item": round(float(np.median(wait[sel])), 2),
+                     "between_items_us": round(float(np.nanmedian(gap[sel])), 2),
                      "end_us_median": round(float(np.median(last_end[sel])), 2),
                      "end_us_max": round(float(np.max(last_end[sel])), 2)})
     return {"timeline": {"workload": f"B={B} {'int4' if resid_fmt == qpd.RESID_INT4 else 'int8'} residual, "
@@ -715,13 +719,13 @@ def main():
             continue
         fmt, ph = formats[fmt_name]
         groups = max(2, min(64, 1024 // bb))
-        m, hm = run_config(device, bb, fmt, ph, max(200, args.steps // 4), 50, groups, args.quant_mode)
+        m, hm = run_config(device, bb, fmt, ph, args.steps, args.warmup, groups, args.quant_mode)
         nb = algorithmic_bytes(bb, H, HV, K, V, fmt, ph)
         sweep[f"B{bb}_{fmt_name}"] = {"us": round(m * 1e3, 3), "host_us": round(hm * 1e3, 3),
                                      "GBps": round(nb / (m * 1e-3) / 1e9, 1),
                                      "frac": round(nb / (m * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
     if not args.no_sweep:   # the headline step with vLLM's bf16 activations and output
-        m, hm = run_config(device, 64, qpd.RESID_INT4, True, max(200, args.steps // 4), 50, 16, args.quant_mode,
+        m, hm = run_config(device, 64, qpd.RESID_INT4, True, args.steps, args.warmup, 16, args.quant_mode,
                            act_dtype=torch.bfloat16)
         nb = algorithmic_bytes(64, H, HV, K, V, qpd.RESID_INT4, True, act_bytes=2)
         sweep["B64_int4_head_bf16act"] = {"us": round(m * 1e3, 3), "host_us": round(hm * 1e3, 3),
