@@ -1,0 +1,93 @@
+"""Randomised GPU parity of the fused decode: many small configurations drawn
+from fixed seeds, each run for two steps on the GPU (through the C ABI) and in
+the oracle from the same pool, compared bit for bit (the outputs and all four
+pool tensors). A draw picks K, V, the GQA ratio, the batch, the residual format
+and scale granularity, the quant mode, the activation / gate / output dtypes,
+the L2-norm flag, the state bits, NULL and out-of-range slot ids and (FAST mode)
+out-of-place destinations; the fixed cases in test_packed_decode_gpu.py cover
+each axis alone."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from carrykernel_amd.vllm_integration import quantized_packed_decode as qpd
+from tests._helpers import make_packed_inputs, make_pool, to_dev
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = (torch.float32, torch.bfloat16, torch.float16)
+
+
+def _draw(seed):
+    rng = np.random.default_rng(seed)
+    K = int(rng.choice([16, 32, 64, 128, 256]))
+    per_head = bool(rng.integers(2))
+    rows_per_inst = 64 // (K // 16)
+    v_max = rows_per_inst * 32 if per_head else 300      # the per-head shapes hold the head in one workgroup
+    V = int(rng.integers(1, min(v_max, 300) + 1))
+    H = int(rng.choice([1, 2, 4]))
+    HV = H * int(rng.choice([1, 2, 3]))
+    B = int(rng.integers(1, 25))
+    resid_fmt = int(rng.choice([qpd.RESID_INT8, qpd.RESID_INT4]))
+    mode = "exact" if rng.random() < 0.3 else "fast"
+    act = DTYPES[int(rng.integers(3))]
+    out_dt = DTYPES[int(rng.integers(3))]
+    return dict(K=K, V=V, H=H, HV=HV, B=B, resid_fmt=resid_fmt, per_head=per_head, mode=mode, act=act,
+                out_dt=out_dt, l2norm=bool(rng.integers(2)), bits=int(rng.integers(2, 9)),
+                dst=mode == "fast" and rng.random() < 0.35, rng=rng)
+
+
+def _expected_out(o_ref, out_dt):
+    if out_dt == torch.bfloat16:
+        return oracle.bf16_round(o_ref)
+    if out_dt == torch.float16:
+        return o_ref.astype(np.float16).astype(np.float32)
+    return o_ref
+
+
+@pytest.mark.parametrize("seed", range(48))
+def test_random_configuration_bit_exact(device, seed):
+    c = _draw(1000 + seed)
+    rng = c.pop("rng")
+    B, H, HV, K, V = c["B"], c["H"], c["HV"], c["K"], c["V"]
+    S = 2 * B + 3 if c["dst"] else B + 3
+    pool = make_pool(S, HV, V, K, c["resid_fmt"], c["per_head"], seed=seed, bits=c["bits"])
+    dpool = to_dev(pool, device)
+    perm = (rng.permutation(S - 1) + 1).astype(np.int32)
+    src = perm[:B].copy()
+    nulls = rng.random(B) < 0.15                      # NULL requests: zeros out, nothing touched
+    src[nulls] = 0
+    if B > 2 and rng.random() < 0.3:                  # one out-of-range id: NaN out, nothing touched
+        src[int(rng.integers(B))] = S + int(rng.integers(3))
+    dst = perm[B:2 * B].copy() if c["dst"] else None
+    print(f"case seed={seed} {({k: (str(v) if isinstance(v, torch.dtype) else v) for k, v in c.items()})}",
+          flush=True)
+    for t in range(2):
+        mixed, a, b, A_log, dt_bias = make_packed_inputs(B, H, HV, K, V, seed=7 * seed + t, dtype=c["act"])
+        # gates in the activation dtype or in fp32, independently
+        if rng.random() < 0.5:
+            a, b = a.float(), b.float()
+        out = torch.empty(B, 1, HV, V, dtype=c["out_dt"], device=device)
+        qpd.quantized_gated_delta_rule_packed_decode(
+            mixed.to(device), a.to(device), b.to(device), A_log.to(device), dt_bias.to(device), K ** -0.5,
+            *dpool, out, torch.from_numpy(src).to(device), use_qk_l2norm_in_kernel=c["l2norm"],
+            resid_fmt=c["resid_fmt"], state_bits=c["bits"], quant_mode=c["mode"],
+            dst_state_indices=None if dst is None else torch.from_numpy(dst).to(device))
+        torch.cuda.synchronize()
+        o_ref = oracle.packed_decode(
+            mixed.float().numpy(), a.float().numpy(), b.float().numpy(), A_log.float().numpy(),
+            dt_bias.float().numpy(), K ** -0.5, *pool, src, H, use_qk_l2norm=c["l2norm"],
+            resid_fmt=c["resid_fmt"], per_head=c["per_head"], state_bits=c["bits"],
+            mode=oracle.MODE_EXACT if c["mode"] == "exact" else oracle.MODE_FAST, dst_indices=dst)
+        np.testing.assert_array_equal(out[:, 0].float().cpu().numpy(), _expected_out(o_ref, c["out_dt"]),
+                                      err_msg=f"out differs at step {t}")
+        for name, d, h in zip(("state_codes", "state_scale", "resid_codes", "resid_scale"), dpool, pool):
+            np.testing.assert_array_equal(d.cpu().numpy(), h, err_msg=f"{name} differs at step {t}")
+        if dst is not None:
+            src, dst = dst, src                       # read back what was written (NULL / bad ids stay put)
+            src = np.where((src > 0) & (src < S), src, 0).astype(np.int32)
+            dst = np.where((dst > 0) & (dst < S), dst, 0).astype(np.int32)
