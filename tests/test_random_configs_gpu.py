@@ -91,3 +91,37 @@ def test_random_configuration_bit_exact(device, seed):
             src, dst = dst, src                       # read back what was written (NULL / bad ids stay put)
             src = np.where((src > 0) & (src < S), src, 0).astype(np.int32)
             dst = np.where((dst > 0) & (dst < S), dst, 0).astype(np.int32)
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_statequant_step_bit_exact(device, seed):
+    """The statequant-layout step (ck_gdn_quant_step through gdn_quant_step_fused)
+    on random shapes, residual formats, quant modes and state bits."""
+    from carrykernel_amd.statequant import kernel as sq
+    from tests.test_statequant_gpu import _random_state, _storage, make_inputs
+
+    rng = np.random.default_rng(5000 + seed)
+    K = int(rng.choice([16, 32, 64, 128]))
+    V = 4 * int(rng.integers(1, 50))                  # the layout's lanes take 4 columns each
+    B, HV = int(rng.integers(1, 4)), int(rng.integers(1, 9))
+    res_fmt = int(rng.integers(4))
+    mode = "exact" if rng.random() < 0.4 else "fast"
+    bits = int(rng.integers(2, 9))
+    print(f"case seed={seed} K={K} V={V} B={B} HV={HV} res={res_fmt} mode={mode} bits={bits}", flush=True)
+    h_int8, scale, e, es = _random_state(B, HV, K, V, res_fmt, seed=seed, bits=bits)
+    _, q, k, v, alpha, beta = make_inputs(1, B, HV, K, V, seed=100 + seed)
+    got = sq.gdn_quant_step_fused(h_int8.to(device), scale.to(device), e.to(device),
+                                  None if es is None else es.to(device), q[0].to(device), k[0].to(device),
+                                  v[0].to(device), alpha[0].to(device), beta[0].to(device), bits=bits,
+                                  res_fmt=res_fmt, quant_mode=mode)
+    torch.cuda.synchronize()
+    ref = oracle.quant_step_kv(h_int8.numpy(), scale.numpy(), _storage(e, res_fmt),
+                               None if es is None else es.numpy(), q[0].numpy(), k[0].numpy(), v[0].numpy(),
+                               alpha[0].numpy(), beta[0].numpy(), bits=bits, res_fmt=res_fmt,
+                               mode=oracle.MODE_EXACT if mode == "exact" else oracle.MODE_FAST)
+    for name, g_, r_ in zip(("o", "h_int8", "scale", "e", "e_scale"), got, ref):
+        if r_ is None:
+            assert g_ is None
+            continue
+        g_np = _storage(g_, res_fmt) if name == "e" else g_.cpu().numpy()
+        np.testing.assert_array_equal(g_np, r_, err_msg=f"{name} differs")
