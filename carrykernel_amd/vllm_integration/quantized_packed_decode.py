@@ -76,7 +76,11 @@ def _check_indices_host(ssm_state_indices: torch.Tensor, num_slots: int) -> None
 
 def _slot_contiguous(t: torch.Tensor) -> bool:
     """Every dim but the slot dim is densely packed (row-major)."""
-    sh, st = t.shape, t.stride()
+    return _dense_after_slot(t.shape, t.stride())
+
+
+def _dense_after_slot(sh, st) -> bool:
+    """_slot_contiguous on a tensor's shape and strides."""
     n = len(sh)
     # the usual dense layouts, without the general loop (this runs per call)
     if n == 4 and st[3] == 1 and st[2] == sh[3] and st[1] == sh[2] * sh[3]:
@@ -128,22 +132,26 @@ def quantized_gated_delta_rule_packed_decode(
         raise RuntimeError("The HIP library is required for the quantized packed decode "
                            "(build it with `python -m carrykernel_amd.build`)")
 
-    # validation and messages follow quantized_packed_decode.py:268-309
-    if mixed_qkv.dim() != 2:
-        raise ValueError(f"mixed_qkv must be 2-D, got {tuple(mixed_qkv.shape)}")
-    if mixed_qkv.stride(-1) != 1:
+    # validation and messages follow quantized_packed_decode.py:268-309; every
+    # tensor's shape and strides are read once (this runs on every call)
+    m_sh, m_st = mixed_qkv.shape, mixed_qkv.stride()
+    sc_sh, sc_st = state_codes.shape, state_codes.stride()
+    rc_sh = resid_codes.shape
+    if len(m_sh) != 2:
+        raise ValueError(f"mixed_qkv must be 2-D, got {tuple(m_sh)}")
+    if m_st[-1] != 1:
         raise ValueError("mixed_qkv must be contiguous in its last dimension")
-    if state_codes.dim() != 4:
-        raise ValueError(f"state_codes must be 4-D, got {tuple(state_codes.shape)}")
-    if state_codes.stride(-1) != 1:
+    if len(sc_sh) != 4:
+        raise ValueError(f"state_codes must be 4-D, got {tuple(sc_sh)}")
+    if sc_st[-1] != 1:
         raise ValueError("state_codes must be contiguous in its last dimension")
     if state_codes.dtype != torch.int8 or resid_codes.dtype != torch.int8:
         raise ValueError("state_codes and resid_codes must be int8 storage")
-    if resid_fmt == RESID_INT4 and resid_codes.shape[-1] * 2 != state_codes.shape[-1]:
+    if resid_fmt == RESID_INT4 and rc_sh[-1] * 2 != sc_sh[-1]:
         raise ValueError(
             "int4 residual must be packed two codes per byte: expected last dim "
-            f"{state_codes.shape[-1] // 2}, got {resid_codes.shape[-1]}")
-    if resid_fmt == RESID_INT8 and resid_codes.shape != state_codes.shape:
+            f"{sc_sh[-1] // 2}, got {rc_sh[-1]}")
+    if resid_fmt == RESID_INT8 and rc_sh != sc_sh:
         raise ValueError("int8 residual must have the same shape as the state")
     if resid_fmt not in (RESID_INT8, RESID_INT4):
         raise ValueError(f"resid_fmt must be RESID_INT8 or RESID_INT4, got {resid_fmt}")
@@ -152,15 +160,16 @@ def quantized_gated_delta_rule_packed_decode(
     if ssm_state_indices.dtype != torch.int32:
         raise ValueError("ssm_state_indices must be int32")
 
-    B = mixed_qkv.shape[0]
-    num_slots, HV, V, K = state_codes.shape
-    if out.shape != (B, 1, HV, V):
-        raise ValueError(f"out must be {(B, 1, HV, V)}, got {tuple(out.shape)}")
+    B = m_sh[0]
+    num_slots, HV, V, K = sc_sh
+    o_sh = out.shape
+    if o_sh != (B, 1, HV, V):
+        raise ValueError(f"out must be {(B, 1, HV, V)}, got {tuple(o_sh)}")
     if not out.is_contiguous():
         raise ValueError("out must be contiguous")
 
     # H is inferred from the packed width, exactly as upstream does.
-    qkv_dim = mixed_qkv.shape[1]
+    qkv_dim = m_sh[1]
     qk_dim = qkv_dim - HV * V
     if qk_dim <= 0 or qk_dim % 2 != 0:
         raise ValueError(f"cannot infer H from mixed_qkv width {qkv_dim}")
@@ -173,26 +182,29 @@ def quantized_gated_delta_rule_packed_decode(
         raise ValueError(f"packed decode supports K in {SUPPORTED_K}, got K={K}")
 
     # checks the reference leaves implicit
-    if state_scale.shape != (num_slots, HV, V) or state_scale.dtype != torch.float32:
+    ss_sh, rs_sh = state_scale.shape, resid_scale.shape
+    if ss_sh != (num_slots, HV, V) or state_scale.dtype != torch.float32:
         raise ValueError(f"state_scale must be float32 {(num_slots, HV, V)}, "
-                         f"got {state_scale.dtype} {tuple(state_scale.shape)}")
+                         f"got {state_scale.dtype} {tuple(ss_sh)}")
     if resid_scale.dtype != torch.float32:
         raise ValueError("resid_scale must be float32")
-    if resid_scale.shape == (num_slots, HV, V):
+    if rs_sh == (num_slots, HV, V):
         rscale_mode = _native.RSCALE_PER_ROW
-    elif resid_scale.shape == (num_slots, HV):
+    elif rs_sh == (num_slots, HV):
         rscale_mode = _native.RSCALE_PER_HEAD
     else:
         raise ValueError(f"resid_scale must be {(num_slots, HV, V)} (per V-row) or "
-                         f"{(num_slots, HV)} (per head), got {tuple(resid_scale.shape)}")
-    if resid_codes.shape[:3] != (num_slots, HV, V):
+                         f"{(num_slots, HV)} (per head), got {tuple(rs_sh)}")
+    if rc_sh[:3] != (num_slots, HV, V):
         raise ValueError("resid_codes must have the state's slot, head and V dims")
-    for name, t in (("state_codes", state_codes), ("state_scale", state_scale),
-                    ("resid_codes", resid_codes), ("resid_scale", resid_scale)):
-        if not _slot_contiguous(t):
+    ss_st, rc_st, rs_st = state_scale.stride(), resid_codes.stride(), resid_scale.stride()
+    for name, sh, st in (("state_codes", sc_sh, sc_st), ("state_scale", ss_sh, ss_st),
+                         ("resid_codes", rc_sh, rc_st), ("resid_scale", rs_sh, rs_st)):
+        if not _dense_after_slot(sh, st):
             raise ValueError(f"{name} must be contiguous within a slot")
-    for name, t in (("a", a), ("b", b)):
-        if t.dim() != 2 or t.shape != (B, HV) or t.stride(-1) != 1:
+    a_st, b_st = a.stride(), b.stride()
+    for name, t, st in (("a", a, a_st), ("b", b, b_st)):
+        if t.shape != (B, HV) or st[-1] != 1:   # the shape test also rejects other ranks
             raise ValueError(f"{name} must be [B, HV] = {(B, HV)} with a contiguous last dim")
     for name, t in (("A_log", A_log), ("dt_bias", dt_bias)):
         if t.shape != (HV,) or t.stride(0) != 1:
@@ -229,16 +241,16 @@ def quantized_gated_delta_rule_packed_decode(
             _check_dst_indices_host(ssm_state_indices[:B], dst_state_indices[:B], num_slots)
 
     L = _native.lib()
-    head = (mixed_qkv.data_ptr(), _native.dtype_code(mixed_qkv, "mixed_qkv"), mixed_qkv.stride(0),
-            a.data_ptr(), _native.dtype_code(a, "a"), a.stride(0),
-            b.data_ptr(), _native.dtype_code(b, "b"), b.stride(0),
+    head = (mixed_qkv.data_ptr(), _native.dtype_code(mixed_qkv, "mixed_qkv"), m_st[0],
+            a.data_ptr(), _native.dtype_code(a, "a"), a_st[0],
+            b.data_ptr(), _native.dtype_code(b, "b"), b_st[0],
             A_log.data_ptr(), _native.dtype_code(A_log, "A_log"),
             dt_bias.data_ptr(), _native.dtype_code(dt_bias, "dt_bias"),
             float(scale),
-            state_codes.data_ptr(), state_codes.stride(0),
-            state_scale.data_ptr(), state_scale.stride(0),
-            resid_codes.data_ptr(), resid_codes.stride(0),
-            resid_scale.data_ptr(), resid_scale.stride(0),
+            state_codes.data_ptr(), sc_st[0],
+            state_scale.data_ptr(), ss_st[0],
+            resid_codes.data_ptr(), rc_st[0],
+            resid_scale.data_ptr(), rs_st[0],
             out.data_ptr(), _native.dtype_code(out, "out"),
             ssm_state_indices.data_ptr(), ssm_state_indices.stride(0))
     tail = (num_slots, B, H, HV, K, V,
