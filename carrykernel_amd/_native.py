@@ -120,8 +120,9 @@ def lib():
             L = ctypes.CDLL(LIB_PATH)
             for name, (res, args) in _SIGNATURES.items():
                 fn = getattr(L, name, None)
-                if fn is None:
-                    continue
+                if fn is None:   # a library built from older sources
+                    raise HipUnavailable(f"{LIB_PATH} does not export {name}; rebuild it "
+                                         "with `python -m carrykernel_amd.build`")
                 fn.restype = res
                 fn.argtypes = args
             if L.ck_abi_version() != ABI_VERSION:
