@@ -299,6 +299,33 @@ def multilayer_token(device, layers=24, B=64, live=None, tokens=20, seed=7):
             "frac": round(nb / (graph_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
 
 
+def ingest_arm(device, slots=257):
+    """State ingest (init_quantized_state's quantization, ck_quantize_rows) of a
+    [slots, HV, V, K] prefill state in fp32 and bf16: reads the state, writes
+    int8 codes and one fp32 scale per row. Buffers rotate over > 256 MB."""
+    from carrykernel_amd import _native
+    L = _native.lib()
+    res = {}
+    rows = slots * HV * V
+    for name, dt, esz in (("ingest_rows_fp32", torch.float32, 4), ("ingest_rows_bf16", torch.bfloat16, 2)):
+        x = torch.randn(slots, HV, V, K, device=device).to(dt)
+        codes = torch.empty(slots, HV, V, K, dtype=torch.int8, device=device)
+        scale = torch.empty(slots, HV, V, device=device)
+        code = _native.dtype_code(x, "x")
+
+        def step(_t, x=x, codes=codes, scale=scale, code=code):
+            _native.check(L.ck_quantize_rows(x.data_ptr(), code, K, rows, K, 127.0, codes.data_ptr(),
+                                             scale.data_ptr(), _native.stream_handle(device)), "ck_quantize_rows")
+
+        ms = _graph_time(device, step, 1, 20, 20)
+        nb = rows * K * (esz + 1) + rows * 4
+        res[name] = {"us": round(ms * 1e3, 2), "bytes": nb, "GBps": round(nb / (ms * 1e-3) / 1e9, 1),
+                     "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+        del x, codes, scale
+        torch.cuda.empty_cache()
+    return res
+
+
 def statequant_bytes(B, HV, K, V, res_fmt):
     """Unique bytes of one statequant-layout step (statequant/kernel.py:379-408):
     int8 codes in/out, residual in/out, per-column state scale in/out (and the
@@ -738,6 +765,7 @@ def main():
         line["multilayer_c5"] = {"full": multilayer_token(device),
                                  "padded": multilayer_token(device, live=48)}
         line["arms"] = arms(device)
+        line["arms"].update(ingest_arm(device))
         # measured copy ceiling at the headline's byte count and for a 1 GiB copy
         at = hbm_copy_peak(device, nbytes)
         big = hbm_copy_peak(device, 1 << 30)

@@ -4,16 +4,104 @@
 //     scale = max(amax, 1e-12) / qmax, code = clamp(rne(x / scale), +-qmax).
 //   ck_quantize_cols: [K, V] matrices, one scale per V-column (amax over K),
 //     per_v_channel_quantize semantics (statequant/kernel.py:99-113).
-// Both use IEEE divisions, so the codes equal torch.round(x / scale).
+// Both divide correctly rounded (IEEE division, or the reciprocal with
+// Markstein's correction), so the codes equal torch.round(x / scale).
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
 
 #include "ck_capi_common.h"
 #include "ck_device.h"
+#include "ck_quant.h"
 
 namespace ck {
 namespace {
 
-// One wavefront per row; lanes stride over K.
+// Rows of K = 16 * LPR (K <= 256), 16-byte aligned: a lane owns 16 consecutive
+// elements of a row (vector loads, one 16-byte store of codes), the LPR lanes
+// of a row take the row amax by DPP, and each element is divided by the row
+// scale through RN(1/s) with Markstein's correction (ck_quant.h, EXACT mode),
+// which is the correctly rounded quotient. |x / s| <= qmax (1 + 2^-23) < qmax
+// + 1/2 since s >= RN(amax / qmax), so no code exceeds qmax and the clamp of
+// the reference never binds. Waves stride over row groups. A lane's 64 (fp32)
+// or 32 (16-bit) bytes are read in 16-byte loads, so one load instruction
+// covers part of every line the wave touches: the loads are cached (the next
+// instruction's bytes are then L2 hits), which measured 1.3x faster than
+// non-temporal loads here.
+template <int LPR, int DT>
+__global__ __launch_bounds__(256) void quantize_rows16_kernel(const char* __restrict__ x, int64_t stride_row_bytes,
+                                                              int64_t rows, float qmax, int8_t* __restrict__ codes,
+                                                              float* __restrict__ scale) {
+  constexpr int RPW = 64 / LPR;  // rows per wave
+  constexpr int K = 16 * LPR;
+  const int lane = threadIdx.x & 63;
+  const int c = lane % LPR;
+  const int g = lane / LPR;
+  const int64_t nwaves = (int64_t)gridDim.x * 4;
+  for (int64_t r0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW; r0 < rows; r0 += nwaves * RPW) {
+    const int64_t row = r0 + g;
+    const bool valid = row < rows;
+    const char* p = x + (valid ? row : rows - 1) * stride_row_bytes + c * 16 * (DT == kF32 ? 4 : 2);
+    float v[16];
+    if constexpr (DT == kF32) {
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const u32x4 w = reinterpret_cast<const u32x4*>(p)[h];
+        v[4 * h] = __uint_as_float(w.x), v[4 * h + 1] = __uint_as_float(w.y);
+        v[4 * h + 2] = __uint_as_float(w.z), v[4 * h + 3] = __uint_as_float(w.w);
+      }
+    } else {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const u32x4 w = reinterpret_cast<const u32x4*>(p)[h];
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[8 * h + 2 * i] = act_decode<DT>(ws[i] & 0xffffu);
+          v[8 * h + 2 * i + 1] = act_decode<DT>(ws[i] >> 16);
+        }
+      }
+    }
+    float am = fabsf(v[0]);
+#pragma unroll
+    for (int j = 1; j < 16; ++j) am = fmaxf(am, fabsf(v[j]));
+    am = group_max<LPR>(am);
+    const float s = fmaxf(am, kEps) / qmax;
+    const float inv = recip_rn(s);
+    uint32_t yb[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) (void)quantize<kExact>(v[j], s, inv, yb[j]);
+    if (valid) {
+      __builtin_nontemporal_store(u32x4{pack_low_bytes(yb[0], yb[1], yb[2], yb[3]),
+                                        pack_low_bytes(yb[4], yb[5], yb[6], yb[7]),
+                                        pack_low_bytes(yb[8], yb[9], yb[10], yb[11]),
+                                        pack_low_bytes(yb[12], yb[13], yb[14], yb[15])},
+                                  reinterpret_cast<u32x4*>(codes + row * K + c * 16));
+      if (c == 0) scale[row] = s;
+    }
+  }
+}
+
+template <int LPR>
+void launch_rows16(const void* x, int dtype, int64_t stride_row, int64_t rows, float qmax, int8_t* codes,
+                   float* scale, hipStream_t stream) {
+  constexpr int RPW = 64 / LPR;
+  const int64_t waves = (rows + RPW - 1) / RPW;
+  const int64_t grid = std::min<int64_t>((waves + 3) / 4, 256 * 32);
+  const int esz = dtype == kF32 ? 4 : 2;
+  const char* xb = static_cast<const char*>(x);
+  if (dtype == kF32)
+    hipLaunchKernelGGL((quantize_rows16_kernel<LPR, kF32>), dim3((unsigned)grid), dim3(256), 0, stream, xb,
+                       stride_row * esz, rows, qmax, codes, scale);
+  else if (dtype == kBF16)
+    hipLaunchKernelGGL((quantize_rows16_kernel<LPR, kBF16>), dim3((unsigned)grid), dim3(256), 0, stream, xb,
+                       stride_row * esz, rows, qmax, codes, scale);
+  else
+    hipLaunchKernelGGL((quantize_rows16_kernel<LPR, kF16>), dim3((unsigned)grid), dim3(256), 0, stream, xb,
+                       stride_row * esz, rows, qmax, codes, scale);
+}
+
+// Any K, any alignment: one wavefront per row; lanes stride over K.
 __global__ __launch_bounds__(256) void quantize_rows_kernel(const void* __restrict__ x, int dtype, int64_t stride_row,
                                                             int64_t rows, int K, float qmax,
                                                             int8_t* __restrict__ codes, float* __restrict__ scale) {
@@ -64,6 +152,20 @@ extern "C" int ck_quantize_rows(const void* x, int x_dtype, int64_t stride_row, 
   if (!(qmax >= 1.0f && qmax <= 127.0f)) return fail(CK_EINVAL, "qmax must be in [1, 127]");
   if (rows == 0) return ok();
   if (!x || !codes || !scale) return fail(CK_EINVAL, "null pointer argument");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int esz = x_dtype == kF32 ? 4 : 2;
+  const bool aligned = ((reinterpret_cast<uintptr_t>(x) | (uintptr_t)(stride_row * esz) |
+                         reinterpret_cast<uintptr_t>(codes)) & 15) == 0;
+  if (aligned && (K == 16 || K == 32 || K == 64 || K == 128 || K == 256)) {
+    switch (K) {
+      case 16: launch_rows16<1>(x, x_dtype, stride_row, rows, qmax, codes, scale, s); break;
+      case 32: launch_rows16<2>(x, x_dtype, stride_row, rows, qmax, codes, scale, s); break;
+      case 64: launch_rows16<4>(x, x_dtype, stride_row, rows, qmax, codes, scale, s); break;
+      case 128: launch_rows16<8>(x, x_dtype, stride_row, rows, qmax, codes, scale, s); break;
+      default: launch_rows16<16>(x, x_dtype, stride_row, rows, qmax, codes, scale, s); break;
+    }
+    return check_launch("ck_quantize_rows");
+  }
   const int64_t grid = (rows + 3) / 4;
   if (grid > 0x7fffffff) return fail(CK_EUNSUPPORTED, "too many rows");
   hipLaunchKernelGGL(quantize_rows_kernel, dim3((unsigned)grid), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),

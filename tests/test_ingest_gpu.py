@@ -52,3 +52,43 @@ def test_init_from_strided_prefill_state(device, S=3, HV=2, V=16, K=64):
     torch.cuda.synchronize()
     for x, y in zip(a, b):
         assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("K", [16, 32, 64, 256])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_init_quantized_state_every_k(device, K, dtype, S=3, HV=2, V=9):
+    """Every decode K through the vectorised row kernel, with a row count
+    (S * HV * V = 54) that leaves the last wave's row group partly empty."""
+    g = torch.Generator().manual_seed(K)
+    h0 = (torch.randn(S, HV, V, K, generator=g) * 0.2).to(dtype)
+    h0[0, 1, 2] = 0.0
+    print(f"case ingest K={K} {dtype}", flush=True)
+    sc, ss, _, _ = qpd.init_quantized_state(S, HV, V, K, device, h0=h0.to(device), resid_fmt=qpd.RESID_INT8)
+    torch.cuda.synchronize()
+    c_ref, s_ref = oracle.quantize_rows(h0.float().numpy(), 127.0)
+    np.testing.assert_array_equal(sc.cpu().numpy(), c_ref)
+    np.testing.assert_array_equal(ss.cpu().numpy(), s_ref)
+
+
+@pytest.mark.parametrize("offset", [0, 1])
+def test_quantize_rows_padded_and_unaligned_rows(device, offset, rows=37, K=128):
+    """ck_quantize_rows through the C ABI on rows with padding between them:
+    16-byte aligned rows take the vectorised kernel, rows starting one fp32
+    element (4 bytes) off alignment the general one; both give the oracle's
+    codes and scales."""
+    from carrykernel_amd import _native
+    L = _native.lib()
+    g = torch.Generator().manual_seed(offset)
+    pitch = K + 12                                   # elements between row starts
+    back = torch.randn(rows * pitch + offset + 16, generator=g).to(device)
+    x = back[offset:offset + rows * pitch].view(rows, pitch)
+    codes = torch.full((rows, K), 99, dtype=torch.int8, device=device)
+    scale = torch.empty(rows, device=device)
+    print(f"case quantize_rows offset={offset}", flush=True)
+    st = L.ck_quantize_rows(x.data_ptr(), 0, pitch, rows, K, 127.0, codes.data_ptr(), scale.data_ptr(),
+                            _native.stream_handle(device))
+    _native.check(st, "ck_quantize_rows")
+    torch.cuda.synchronize()
+    c_ref, s_ref = oracle.quantize_rows(np.ascontiguousarray(x[:, :K].cpu().numpy()), 127.0)
+    np.testing.assert_array_equal(codes.cpu().numpy(), c_ref)
+    np.testing.assert_array_equal(scale.cpu().numpy(), s_ref)
