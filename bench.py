@@ -326,6 +326,37 @@ def ingest_arm(device, slots=257):
     return res
 
 
+def slot_ops_arm(device, n=256):
+    """The engine-side slot operations (ck_pool_copy_slots, ck_pool_reset_slots)
+    on an int4 / per-head pool of HV=32, K=V=128: copy n random slots to n
+    others of a 4n+1-slot pool (slot bytes read and written), reset n slots
+    (written)."""
+    res = {}
+    S = 4 * n + 1
+    pool = qpd.init_quantized_state(S, HV, V, K, device, resid_fmt=qpd.RESID_INT4, per_head_resid_scale=True)
+    slot_bytes = qpd.state_bytes_per_slot(HV, V, K, True, resid_fmt=qpd.RESID_INT4, per_head_resid_scale=True)
+    perm = torch.randperm(S - 1, generator=torch.Generator().manual_seed(11)) + 1
+    groups = [perm[i * n:(i + 1) * n].to(torch.int32).to(device) for i in range(4)]
+
+    def copy_step(t):
+        qpd.copy_quantized_state(pool, groups[t % 4], pool, groups[(t + 1) % 4])
+
+    def reset_step(t):
+        qpd.reset_quantized_state(pool, groups[t % 4])
+
+    ms = _graph_time(device, copy_step, 3, 20, 20)
+    nb = 2 * n * slot_bytes
+    res["pool_copy_slots"] = {"us": round(ms * 1e3, 2), "bytes": nb, "GBps": round(nb / (ms * 1e-3) / 1e9, 1),
+                              "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+    ms = _graph_time(device, reset_step, 4, 20, 20)
+    nb = n * slot_bytes
+    res["pool_reset_slots"] = {"us": round(ms * 1e3, 2), "bytes": nb, "GBps": round(nb / (ms * 1e-3) / 1e9, 1),
+                               "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+    del pool
+    torch.cuda.empty_cache()
+    return res
+
+
 def statequant_bytes(B, HV, K, V, res_fmt):
     """Unique bytes of one statequant-layout step (statequant/kernel.py:379-408):
     int8 codes in/out, residual in/out, per-column state scale in/out (and the
@@ -766,6 +797,7 @@ def main():
                                  "padded": multilayer_token(device, live=48)}
         line["arms"] = arms(device)
         line["arms"].update(ingest_arm(device))
+        line["arms"].update(slot_ops_arm(device))
         # measured copy ceiling at the headline's byte count and for a 1 GiB copy
         at = hbm_copy_peak(device, nbytes)
         big = hbm_copy_peak(device, 1 << 30)

@@ -58,26 +58,89 @@ __global__ __launch_bounds__(kThreads) void pool_slots_kernel(PoolView src, Pool
   char* out = dst.base[reg] + d * dst.stride[reg];
   const char* in = reset ? nullptr : src.base[reg] + s * src.stride[reg];
   const int64_t first = ((int64_t)blockIdx.x * kUnitsPerThread) * kThreads + threadIdx.x;
+  // every load of the thread is issued before its first store: the source and
+  // destination may be the same pool, so the compiler could not hoist a load
+  // above an earlier store, and one unit at a time would be in flight
   if (plan.vec16[reg]) {
     const int64_t n = bytes >> 4;
+    u32x4_t v[kUnitsPerThread];
 #pragma unroll
     for (int u = 0; u < kUnitsPerThread; ++u) {
       const int64_t i = first + (int64_t)u * kThreads;
-      if (i < n) {
-        const u32x4_t v = reset ? u32x4_t{0u, 0u, 0u, 0u}
-                                : __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(in) + i);
-        __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(out) + i);
-      }
+      v[u] = (reset || i >= n) ? u32x4_t{0u, 0u, 0u, 0u}
+                               : __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(in) + i);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnitsPerThread; ++u) {
+      const int64_t i = first + (int64_t)u * kThreads;
+      if (i < n) __builtin_nontemporal_store(v[u], reinterpret_cast<u32x4_t*>(out) + i);
     }
   } else {
     const int64_t n = bytes >> 2;
+    uint32_t v[kUnitsPerThread];
 #pragma unroll
     for (int u = 0; u < kUnitsPerThread; ++u) {
       const int64_t i = first + (int64_t)u * kThreads;
-      if (i < n) {
-        const uint32_t v = reset ? 0u : reinterpret_cast<const uint32_t*>(in)[i];
-        reinterpret_cast<uint32_t*>(out)[i] = v;
+      v[u] = (reset || i >= n) ? 0u : reinterpret_cast<const uint32_t*>(in)[i];
+    }
+#pragma unroll
+    for (int u = 0; u < kUnitsPerThread; ++u) {
+      const int64_t i = first + (int64_t)u * kThreads;
+      if (i < n) reinterpret_cast<uint32_t*>(out)[i] = v[u];
+    }
+  }
+}
+
+// Every region in 16-byte units (the usual layout): the four regions of a
+// slot are one range of U units (state, state scales, residual, residual
+// scales: units [p0, p1), [p1, p2), [p2, p3), [p3, U)), a pair's range is
+// split over blockIdx.x in runs of kThreads * kFlatUnits consecutive units,
+// so no workgroup is launched without work. Each thread issues all its loads
+// before its stores (the source and destination may be the same pool, so the
+// compiler could not hoist a load above an earlier store).
+constexpr int kFlatUnits = 8;
+
+struct FlatPlan {
+  int64_t p[kRegions + 1];  // region starts in units; p[kRegions] = units per slot
+};
+
+__global__ __launch_bounds__(kThreads) void pool_slots_flat_kernel(PoolView src, PoolView dst, FlatPlan f,
+                                                                   const int32_t* __restrict__ src_ids,
+                                                                   const int32_t* __restrict__ dst_ids, int reset) {
+  const int pair = (int)blockIdx.y;
+  const int64_t d = dst_ids[pair];
+  if (d <= 0 || d >= dst.num_slots) return;  // whole workgroup
+  int64_t s = 0;
+  if (!reset) {
+    s = src_ids[pair];
+    if (s <= 0 || s >= src.num_slots) return;
+  }
+  const int64_t first = (int64_t)blockIdx.x * kThreads * kFlatUnits + threadIdx.x;
+  // the regions are walked in an unrolled loop, so each region's base and
+  // stride stay uniform kernel arguments; a unit is handled in its region
+  u32x4_t v[kFlatUnits];
+#pragma unroll
+  for (int u = 0; u < kFlatUnits; ++u) v[u] = u32x4_t{0u, 0u, 0u, 0u};
+  if (!reset) {
+#pragma unroll
+    for (int r = 0; r < kRegions; ++r) {
+      const char* in = src.base[r] + s * src.stride[r];
+#pragma unroll
+      for (int u = 0; u < kFlatUnits; ++u) {
+        const int64_t w = first + (int64_t)u * kThreads;
+        if (w >= f.p[r] && w < f.p[r + 1])
+          v[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(in) + (w - f.p[r]));
       }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kRegions; ++r) {
+    char* out = dst.base[r] + d * dst.stride[r];
+#pragma unroll
+    for (int u = 0; u < kFlatUnits; ++u) {
+      const int64_t w = first + (int64_t)u * kThreads;
+      if (w >= f.p[r] && w < f.p[r + 1])
+        __builtin_nontemporal_store(v[u], reinterpret_cast<u32x4_t*>(out) + (w - f.p[r]));
     }
   }
 }
@@ -115,6 +178,16 @@ int launch(const PoolView& src, const PoolView& dst, RegionPlan plan, const int3
     max_units = units > max_units ? units : max_units;
   }
   if (n == 0 || max_units == 0) return ok();
+  if (plan.vec16[0] && plan.vec16[1] && plan.vec16[2] && plan.vec16[3]) {
+    FlatPlan f;
+    f.p[0] = 0;
+    for (int r = 0; r < kRegions; ++r) f.p[r + 1] = f.p[r] + (plan.bytes[r] >> 4);
+    const int64_t runs = (f.p[kRegions] + (int64_t)kThreads * kFlatUnits - 1) / ((int64_t)kThreads * kFlatUnits);
+    if (runs > 0x7fffffff || n > 65535) return fail(CK_EUNSUPPORTED, "%s: too many slots or too large a slot", what);
+    hipLaunchKernelGGL(pool_slots_flat_kernel, dim3((unsigned)runs, (unsigned)n), dim3(kThreads), 0,
+                       reinterpret_cast<hipStream_t>(stream), src, dst, f, src_ids, dst_ids, reset);
+    return check_launch(what);
+  }
   const int64_t chunks = (max_units + (int64_t)kThreads * kUnitsPerThread - 1) / ((int64_t)kThreads * kUnitsPerThread);
   if (chunks > 0x7fffffff || n > 65535) return fail(CK_EUNSUPPORTED, "%s: too many slots or too large a slot", what);
   hipLaunchKernelGGL(pool_slots_kernel, dim3((unsigned)chunks, (unsigned)n, kRegions), dim3(kThreads), 0,
