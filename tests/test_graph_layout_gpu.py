@@ -113,3 +113,44 @@ def test_padded_slot_strides(device, resid_fmt, per_head, H=4, HV=8, K=128, V=12
         np.testing.assert_array_equal(view.cpu().numpy(), h)
         tail = big[:, big.shape[1] - pad:].cpu()
         assert torch.all(tail == (77 if big.dtype == torch.int8 else -5.0)), "padding between slots was written"
+
+
+def test_concurrent_calls_from_two_threads(device, H=8, HV=16, K=128, V=128, B=16, T=12):
+    """The C ABI keeps no per-call state outside its arguments (the occupancy
+    cache is filled once under a lock): two host threads, each driving its own
+    pool on its own stream, give the same results as the same steps run one
+    after the other."""
+    import threading
+
+    def run(pool_h, seed, stream, outs):
+        pool = [torch.from_numpy(np.array(x, copy=True)).to(device) for x in pool_h]
+        idx = torch.arange(1, B + 1, dtype=torch.int32, device=device)
+        steps = [[x.to(device) for x in make_packed_inputs(B, H, HV, K, V, seed=seed + t)] for t in range(T)]
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            for mixed, a, b, A_log, dt_bias in steps:
+                out = torch.empty(B, 1, HV, V, device=device)
+                qpd.quantized_gated_delta_rule_packed_decode(mixed, a, b, A_log, dt_bias, 0.1, *pool, out, idx,
+                                                             resid_fmt=qpd.RESID_INT4)
+                outs.append(out)
+        stream.synchronize()
+        outs.extend(pool)
+
+    pools = [make_pool(B + 1, HV, V, K, qpd.RESID_INT4, True, seed=s) for s in (81, 82)]
+    # sequential reference
+    ref = [[], []]
+    for i in range(2):
+        run(pools[i], 100 * i, torch.cuda.Stream(device), ref[i])
+    print("case two host threads, two streams", flush=True)
+    got = [[], []]
+    threads = [threading.Thread(target=run, args=(pools[i], 100 * i, torch.cuda.Stream(device), got[i]))
+               for i in range(2)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=60)
+        assert not th.is_alive()
+    for i in range(2):
+        assert len(got[i]) == len(ref[i])
+        for x, y in zip(got[i], ref[i]):
+            assert torch.equal(x, y)
