@@ -125,3 +125,47 @@ def test_random_statequant_step_bit_exact(device, seed):
             continue
         g_np = _storage(g_, res_fmt) if name == "e" else g_.cpu().numpy()
         np.testing.assert_array_equal(g_np, r_, err_msg=f"{name} differs")
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_float_state_arm_bit_exact(device, seed):
+    """The unquantized-state comparison arm (ck_gdn_packed_decode_float_state)
+    on random shapes, fp32 or bf16 state, fp32 or bf16 activations, the L2-norm
+    flag and NULL ids, two steps against the oracle."""
+    from carrykernel_amd import _native
+
+    rng = np.random.default_rng(9000 + seed)
+    K = int(rng.choice([16, 32, 64, 128, 256]))
+    V = int(rng.integers(1, 200))
+    H = int(rng.choice([1, 2, 4]))
+    HV = H * int(rng.choice([1, 2]))
+    B = int(rng.integers(1, 40))
+    sdt = torch.bfloat16 if rng.random() < 0.5 else torch.float32
+    act = torch.bfloat16 if rng.random() < 0.5 else torch.float32
+    l2 = bool(rng.integers(2))
+    S = B + 2
+    print(f"case seed={seed} K={K} V={V} H={H} HV={HV} B={B} state={sdt} act={act} l2={l2}", flush=True)
+    state = (torch.from_numpy(rng.standard_normal((S, HV, V, K)).astype(np.float32)) * 0.1).to(sdt)
+    ref_state = state.float().numpy().copy()
+    idx = (rng.permutation(S - 1)[:B] + 1).astype(np.int32)
+    idx[rng.random(B) < 0.15] = 0
+    dstate = state.to(device)
+    L = _native.lib()
+    for t in range(2):
+        mixed, a, b, A_log, dt_bias = make_packed_inputs(B, H, HV, K, V, seed=31 * seed + t, dtype=act)
+        code = _native.dtype_code(mixed, "mixed")
+        dm, da, db, dA, dd = (x.to(device) for x in (mixed, a, b, A_log, dt_bias))
+        out = torch.empty(B, 1, HV, V, device=device)
+        didx = torch.from_numpy(idx).to(device)
+        rc = L.ck_gdn_packed_decode_float_state(
+            dm.data_ptr(), code, dm.stride(0), da.data_ptr(), code, da.stride(0), db.data_ptr(), code, db.stride(0),
+            dA.data_ptr(), code, dd.data_ptr(), code, K ** -0.5, dstate.data_ptr(), 0 if sdt == torch.float32 else 1,
+            dstate.stride(0), out.data_ptr(), 0, didx.data_ptr(), 1, S, B, H, HV, K, V, int(l2),
+            _native.stream_handle(device))
+        _native.check(rc, "float_state")
+        torch.cuda.synchronize()
+        o_ref = oracle.packed_decode_float_state(mixed.float().numpy(), a.float().numpy(), b.float().numpy(),
+                                                 A_log.float().numpy(), dt_bias.float().numpy(), K ** -0.5,
+                                                 ref_state, idx, H, bf16=sdt == torch.bfloat16, use_qk_l2norm=l2)
+        np.testing.assert_array_equal(out[:, 0].cpu().numpy(), o_ref, err_msg=f"out differs at step {t}")
+        np.testing.assert_array_equal(dstate.float().cpu().numpy(), ref_state, err_msg=f"state differs at step {t}")
