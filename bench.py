@@ -323,6 +323,22 @@ def ingest_arm(device, slots=257):
                      "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
         del x, codes, scale
         torch.cuda.empty_cache()
+    # the statequant layout's per-V-column quantization (per_v_channel_quantize,
+    # ck_quantize_cols) of a [slots, HV, K, V] fp32 state
+    x = torch.randn(slots, HV, K, V, device=device)
+    codes = torch.empty(slots, HV, K, V, dtype=torch.int8, device=device)
+    scale = torch.empty(slots, HV, V, device=device)
+
+    def cstep(_t):
+        _native.check(L.ck_quantize_cols(x.data_ptr(), slots * HV, K, V, 127.0, codes.data_ptr(), scale.data_ptr(),
+                                         _native.stream_handle(device)), "ck_quantize_cols")
+
+    ms = _graph_time(device, cstep, 1, 20, 20)
+    nb = slots * HV * K * V * 5 + slots * HV * V * 4
+    res["ingest_cols_fp32"] = {"us": round(ms * 1e3, 2), "bytes": nb, "GBps": round(nb / (ms * 1e-3) / 1e9, 1),
+                               "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+    del x, codes, scale
+    torch.cuda.empty_cache()
     return res
 
 

@@ -120,8 +120,54 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const void* __restri
   if (lane == 0) scale[row] = s;
 }
 
-// One thread per (matrix, V-column); consecutive threads take consecutive
-// columns so every K-row access is coalesced.
+// [M, K, V] matrices with K in {16, 32, 64, 128}, V % 4 == 0, 16-byte aligned:
+// a lane owns 4 consecutive columns over K/8 rows (its whole slice stays in
+// registers, no second read), lane = column group * 8 + K-slice, so one load
+// instruction reads 8 rows of 128 contiguous bytes; the column amax combines
+// the 8 K-slice lanes by DPP, the division is the exact reciprocal form of
+// quantize_rows16_kernel, and each row's 4 codes go out as one dword. A
+// workgroup of 4 waves covers 128 columns of one matrix.
+template <int K>
+__global__ __launch_bounds__(256) void quantize_cols4_kernel(const float* __restrict__ x, int V, float qmax,
+                                                             int8_t* __restrict__ codes, float* __restrict__ scale) {
+  constexpr int R = K / 8;  // rows per lane
+  const int lane = threadIdx.x & 63;
+  const int kc = lane & 7;
+  const int col0 = (int)blockIdx.x * 128 + (int)(threadIdx.x >> 6) * 32 + (lane >> 3) * 4;
+  const int64_t m = blockIdx.y;
+  const bool valid = col0 < V;
+  const int col = valid ? col0 : V - 4;  // re-read the last group (no store)
+  const float* xm = x + m * K * V + (int64_t)(kc * R) * V + col;
+  float v[R][4];
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const float4 f = *reinterpret_cast<const float4*>(xm + (int64_t)j * V);
+    v[j][0] = f.x, v[j][1] = f.y, v[j][2] = f.z, v[j][3] = f.w;
+  }
+  float s[4], inv[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    float am = fabsf(v[0][c]);
+#pragma unroll
+    for (int j = 1; j < R; ++j) am = fmaxf(am, fabsf(v[j][c]));
+    am = group_max<8>(am);
+    s[c] = fmaxf(am, kEps) / qmax;
+    inv[c] = recip_rn(s[c]);
+  }
+  if (!valid) return;
+  int8_t* cm = codes + m * K * V + (int64_t)(kc * R) * V + col;
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    uint32_t yb[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) (void)quantize<kExact>(v[j][c], s[c], inv[c], yb[c]);
+    *reinterpret_cast<uint32_t*>(cm + (int64_t)j * V) = pack_low_bytes(yb[0], yb[1], yb[2], yb[3]);
+  }
+  if (kc == 0) *reinterpret_cast<float4*>(scale + m * V + col) = make_float4(s[0], s[1], s[2], s[3]);
+}
+
+// Any shape: one thread per (matrix, V-column); consecutive threads take
+// consecutive columns so every K-row access is coalesced.
 __global__ __launch_bounds__(256) void quantize_cols_kernel(const float* __restrict__ x, int64_t M, int K, int V,
                                                             float qmax, int8_t* __restrict__ codes,
                                                             float* __restrict__ scale) {
@@ -180,6 +226,19 @@ extern "C" int ck_quantize_cols(const float* x, int64_t M, int K, int V, float q
   if (!(qmax >= 1.0f && qmax <= 127.0f)) return fail(CK_EINVAL, "qmax must be in [1, 127]");
   if (M == 0) return ok();
   if (!x || !codes || !scale) return fail(CK_EINVAL, "null pointer argument");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool aligned = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(codes) |
+                         reinterpret_cast<uintptr_t>(scale)) & 15) == 0;
+  if (aligned && V % 4 == 0 && M <= 65535 && (K == 16 || K == 32 || K == 64 || K == 128)) {
+    const dim3 grid((unsigned)((V + 127) / 128), (unsigned)M);
+    switch (K) {
+      case 16: hipLaunchKernelGGL(quantize_cols4_kernel<16>, grid, dim3(256), 0, s, x, V, qmax, codes, scale); break;
+      case 32: hipLaunchKernelGGL(quantize_cols4_kernel<32>, grid, dim3(256), 0, s, x, V, qmax, codes, scale); break;
+      case 64: hipLaunchKernelGGL(quantize_cols4_kernel<64>, grid, dim3(256), 0, s, x, V, qmax, codes, scale); break;
+      default: hipLaunchKernelGGL(quantize_cols4_kernel<128>, grid, dim3(256), 0, s, x, V, qmax, codes, scale); break;
+    }
+    return check_launch("ck_quantize_cols");
+  }
   const int64_t grid = (M * V + 255) / 256;
   if (grid > 0x7fffffff) return fail(CK_EUNSUPPORTED, "too many columns");
   hipLaunchKernelGGL(quantize_cols_kernel, dim3((unsigned)grid), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),

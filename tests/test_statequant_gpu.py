@@ -193,3 +193,26 @@ def test_batch8_step(device):
                                res_fmt=sq.RES_INT8)
     for g_, r_ in zip(got, ref):
         np.testing.assert_array_equal(g_.cpu().numpy(), r_)
+
+
+@pytest.mark.parametrize("K", [16, 32, 64, 128])
+@pytest.mark.parametrize("V", [4, 36, 200, 7])
+def test_per_v_channel_quantize_shapes_and_ties(device, K, V):
+    """Every K of the vectorised column kernel, V below and above one
+    workgroup's 128 columns and not a multiple of 32 (idle lanes), and V = 7
+    (the general kernel); column 0 holds exact .5 ties at scale 1.0 (amax 127),
+    which round to even as torch.round does."""
+    g = torch.Generator().manual_seed(K * 1000 + V)
+    x = torch.randn(5, K, V, generator=g) * 0.7
+    ties = torch.tensor([2.5, -3.5, 0.5, -0.5, 1.5, 126.5])
+    x[:, :len(ties), 0] = ties
+    x[:, len(ties), 0] = 127.0
+    x[:, len(ties) + 1:, 0] = 0.25
+    print(f"case per_v_channel_quantize K={K} V={V}", flush=True)
+    codes, scale, _ = sq.per_v_channel_quantize(x.to(device), 8)
+    torch.cuda.synchronize()
+    c_ref, s_ref = oracle.quantize_cols(x.numpy(), 127.0)
+    np.testing.assert_array_equal(codes.cpu().numpy(), c_ref)
+    np.testing.assert_array_equal(scale.cpu().numpy(), s_ref)
+    assert torch.all(scale.cpu()[:, 0] == 1.0)
+    assert codes.cpu()[0, :len(ties), 0].tolist() == [2, -4, 0, 0, 2, 126]
