@@ -169,3 +169,64 @@ def test_random_float_state_arm_bit_exact(device, seed):
                                                  ref_state, idx, H, bf16=sdt == torch.bfloat16, use_qk_l2norm=l2)
         np.testing.assert_array_equal(out[:, 0].cpu().numpy(), o_ref, err_msg=f"out differs at step {t}")
         np.testing.assert_array_equal(dstate.float().cpu().numpy(), ref_state, err_msg=f"state differs at step {t}")
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_slot_copy_and_reset(device, seed):
+    """ck_pool_copy_slots / ck_pool_reset_slots on random pool shapes, residual
+    formats and scale granularities, within one pool and between two, with
+    NULL and out-of-range ids (skipped pairs) and, for a third of the draws,
+    slots with padding between them (the 4-byte path); checked byte for byte
+    against the same copies on the host."""
+    rng = np.random.default_rng(12000 + seed)
+    K = int(rng.choice([16, 32, 64, 128, 256]))
+    HV, V = int(rng.integers(1, 9)), int(rng.integers(1, 80))
+    resid_fmt = int(rng.choice([qpd.RESID_INT8, qpd.RESID_INT4]))
+    per_head = bool(rng.integers(2))
+    S, S2 = int(rng.integers(4, 20)), int(rng.integers(3, 12))
+    padded = rng.random() < 0.33
+    print(f"case seed={seed} K={K} HV={HV} V={V} resid={resid_fmt} per_head={per_head} S={S} S2={S2} padded={padded}",
+          flush=True)
+
+    def dev_pool(h):
+        if not padded:
+            return to_dev(h, device)
+        out = []
+        for x in h:
+            n = x[0].size
+            back = torch.zeros((x.shape[0], n + 4), dtype=torch.from_numpy(x[:1]).dtype, device=device)
+            v = back[:, :n].view(x.shape)
+            v.copy_(torch.from_numpy(x).to(device))
+            out.append(v)
+        return out
+
+    a_h = make_pool(S, HV, V, K, resid_fmt, per_head, seed=seed)
+    b_h = make_pool(S2, HV, V, K, resid_fmt, per_head, seed=seed + 100)
+    a_d, b_d = dev_pool(a_h), dev_pool(b_h)
+    n = int(rng.integers(1, 6))
+    src = rng.integers(-1, S + 2, size=n).astype(np.int32)          # some ids out of range or NULL
+    dst = rng.choice(np.arange(1, S2), size=min(n, S2 - 1), replace=False).astype(np.int32)
+    src = src[:len(dst)]
+    qpd.copy_quantized_state(a_d, torch.from_numpy(src).to(device), b_d, torch.from_numpy(dst).to(device))
+    for s_, d_ in zip(src, dst):
+        if 0 < s_ < S:
+            for x, y in zip(a_h, b_h):
+                y[d_] = x[s_]
+    # within one pool: disjoint source and destination sets
+    perm = rng.permutation(S - 1) + 1
+    m = int(rng.integers(1, (S - 1) // 2 + 1))
+    s2, d2 = perm[:m].astype(np.int32), perm[m:2 * m].astype(np.int32)
+    qpd.copy_quantized_state(a_d, torch.from_numpy(s2).to(device), a_d, torch.from_numpy(d2).to(device))
+    for s_, d_ in zip(s2, d2):
+        for x in a_h:
+            x[d_] = x[s_]
+    r = rng.integers(0, S + 2, size=3).astype(np.int32)
+    qpd.reset_quantized_state(a_d, torch.from_numpy(r).to(device))
+    for i in r:
+        if 0 < i < S:
+            for x in a_h:
+                x[i] = 0
+    torch.cuda.synchronize()
+    for pool_d, pool_h, tag in ((a_d, a_h, "pool a"), (b_d, b_h, "pool b")):
+        for name, d, h in zip(("state_codes", "state_scale", "resid_codes", "resid_scale"), pool_d, pool_h):
+            np.testing.assert_array_equal(d.cpu().numpy(), h, err_msg=f"{tag} {name}")
