@@ -111,7 +111,10 @@ __global__ __launch_bounds__(kThreads) void quant_step_kernel(const StepParams p
   const float beta = p.beta[w];
 
   uint32_t cw[RPS];
-  float ev[RPS][4];
+  // the residual stays in its stored form until t = h + e (16, 32 or 64
+  // registers for 8-bit, fp16 and fp32 residuals instead of 64 floats)
+  constexpr int EWD = RES == kResFp32 ? 4 : RES == kResFp16 ? 2 : 1;
+  uint32_t ew[RPS][EWD];
   float4 sc = make_float4(0.f, 0.f, 0.f, 0.f), esc = make_float4(0.f, 0.f, 0.f, 0.f),
          vv = make_float4(0.f, 0.f, 0.f, 0.f);
   float kk[RPS], qq[RPS];
@@ -129,22 +132,15 @@ __global__ __launch_bounds__(kThreads) void quant_step_kernel(const StepParams p
       const int64_t i = mb + (int64_t)(r0 + r) * p.V + c0;
       cw[r] = *reinterpret_cast<const uint32_t*>(p.h_in + i);
       if constexpr (RES == kResFp32) {
-        const float4 e4 = *reinterpret_cast<const float4*>(static_cast<const float*>(p.e_in) + i);
-        ev[r][0] = e4.x, ev[r][1] = e4.y, ev[r][2] = e4.z, ev[r][3] = e4.w;
+        const uint4 e4 = *reinterpret_cast<const uint4*>(static_cast<const float*>(p.e_in) + i);
+        ew[r][0] = e4.x, ew[r][1] = e4.y, ew[r][2] = e4.z, ew[r][3] = e4.w;
       } else if constexpr (RES == kResFp16) {
         const uint2 e2 = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.e_in) + i);
-        ev[r][0] = half_bits_to_f32(e2.x & 0xffffu), ev[r][1] = half_bits_to_f32(e2.x >> 16);
-        ev[r][2] = half_bits_to_f32(e2.y & 0xffffu), ev[r][3] = half_bits_to_f32(e2.y >> 16);
+        ew[r][0] = e2.x, ew[r][1] = e2.y;
       } else if constexpr (RES == kResFp8) {
-        const uint32_t e1 = *reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(p.e_in) + i);
-        ev[r][0] = __builtin_amdgcn_cvt_f32_bf8((int)e1, 0);
-        ev[r][1] = __builtin_amdgcn_cvt_f32_bf8((int)e1, 1);
-        ev[r][2] = __builtin_amdgcn_cvt_f32_bf8((int)e1, 2);
-        ev[r][3] = __builtin_amdgcn_cvt_f32_bf8((int)e1, 3);
+        ew[r][0] = *reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(p.e_in) + i);
       } else {
-        const uint32_t e1 = *reinterpret_cast<const uint32_t*>(static_cast<const int8_t*>(p.e_in) + i);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) ev[r][j] = code_i8(e1, j);
+        ew[r][0] = *reinterpret_cast<const uint32_t*>(static_cast<const int8_t*>(p.e_in) + i);
       }
     }
   } else {
@@ -152,7 +148,7 @@ __global__ __launch_bounds__(kThreads) void quant_step_kernel(const StepParams p
     for (int r = 0; r < RPS; ++r) {
       cw[r] = 0;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) ev[r][j] = 0.0f;
+      for (int j = 0; j < EWD; ++j) ew[r][j] = 0u;   // decodes to +0 in every format
     }
   }
   const float scv[4] = {sc.x, sc.y, sc.z, sc.w};
@@ -192,15 +188,31 @@ __global__ __launch_bounds__(kThreads) void quant_step_kernel(const StepParams p
     for (int r = 1; r < RPS; ++r) acc = fmaf(h[r][j], qq[r], acc);
     red[1][ks][lc + j] = acc;
   }
-  // t = h + e
+  // t = h + e (the residual decoded here)
 #pragma unroll
   for (int r = 0; r < RPS; ++r) {
+    float ev[4];
+    if constexpr (RES == kResFp32) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) ev[j] = __uint_as_float(ew[r][j]);
+    } else if constexpr (RES == kResFp16) {
+      ev[0] = half_bits_to_f32(ew[r][0] & 0xffffu), ev[1] = half_bits_to_f32(ew[r][0] >> 16);
+      ev[2] = half_bits_to_f32(ew[r][1] & 0xffffu), ev[3] = half_bits_to_f32(ew[r][1] >> 16);
+    } else if constexpr (RES == kResFp8) {
+      ev[0] = __builtin_amdgcn_cvt_f32_bf8((int)ew[r][0], 0);
+      ev[1] = __builtin_amdgcn_cvt_f32_bf8((int)ew[r][0], 1);
+      ev[2] = __builtin_amdgcn_cvt_f32_bf8((int)ew[r][0], 2);
+      ev[3] = __builtin_amdgcn_cvt_f32_bf8((int)ew[r][0], 3);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) ev[j] = code_i8(ew[r][0], j);
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       if constexpr (RES == kResInt8) {
-        h[r][j] = madd<MODE>(ev[r][j], escv[j], h[r][j]);
+        h[r][j] = madd<MODE>(ev[j], escv[j], h[r][j]);
       } else {
-        h[r][j] = h[r][j] + ev[r][j];
+        h[r][j] = h[r][j] + ev[j];
       }
     }
   }
