@@ -248,3 +248,13 @@ def test_slot_contiguity_check_matches_its_definition():
         cases.append(torch.empty(1000).as_strided(shape, strides))
     for t in cases:
         assert qpd._slot_contiguous(t) == rule(t), (tuple(t.shape), t.stride())
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU and says so for --gpus N > 1 (exit status 2)."""
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, os.path.join(REPO, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=300)
+    assert r.returncode == 2
+    assert "only --gpus 1" in r.stderr and r.stdout == ""
