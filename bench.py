@@ -112,38 +112,201 @@ def warm_state(S, device, seed):
     return state
 
 
-def cpu_baseline(B, resid_fmt, per_head, seconds=12.0):
-    """The CPU oracle (C, OpenMP over (request, head)) on the same workload
-    shape, timed on this host for about `seconds`."""
-    import numpy as np
-    import oracle
-    nthreads = len(os.sched_getaffinity(0))
-    nthreads = min(nthreads, 16)
-    S = B + 1
-    rng = np.random.default_rng(0)
-    h0 = (rng.standard_normal((S, HV, V, K)) * 0.1).astype(np.float32)
-    sc, ss = oracle.quantize_rows(h0)
-    rc = np.zeros((S, HV, V, K // 2 if resid_fmt == qpd.RESID_INT4 else K), np.int8)
-    rs = np.zeros((S, HV) if per_head else (S, HV, V), np.float32)
-    sets, A_log, dt_bias = make_step_inputs(B, 2, "cpu", 5)
-    idx = np.arange(1, B + 1, dtype=np.int32)
-    steps = 0
-    t0 = time.perf_counter()
-    while True:
-        mixed, a, b = sets[steps % 2]
-        oracle.packed_decode(mixed.numpy(), a.numpy(), b.numpy(), A_log.numpy(), dt_bias.numpy(), 1.0,
-                             sc, ss, rc, rs, idx, H, resid_fmt=resid_fmt, per_head=per_head,
-                             nthreads=nthreads)
-        steps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or steps >= 5000:
-            break
-    us = el / steps * 1e6
-    gbps = algorithmic_bytes(B, H, HV, K, V, resid_fmt, per_head) / (us * 1e-6) / 1e9
-    return {"value": round(gbps, 3), "unit": "GB/s", "us_per_step": round(us, 1), "cores": nthreads,
-            "kind": "port",
-            "sample": f"{steps} steps of the B={B} workload through the C oracle (oracle/gdn_oracle.c, "
-                      f"OpenMP, {nthreads} threads), {el:.1f} s"}
+class CpuLeg:
+    """The CPU leg of the bench, the only part of it that loads oracle/.
+
+    * The reference's CPU path timed on this host: oracle/torch_path.py, a
+      torch restatement of gdn_quant_step_torch (statequant/kernel.py:149-178)
+      in the vLLM layout with int4 nibble packing, on the same workload shape,
+      with torch using every core this process may run on.
+    * Every timed GPU configuration checked before it is timed: one GPU step on
+      the configuration's own buffers and code path, its touched slots and
+      outputs compared bit for bit with the C oracle on host copies of the
+      same inputs (as experiments/kernel_bench.py:77-91,158-163 checks each
+      configuration against its torch path). A mismatch makes the bench fail.
+    """
+
+    def __init__(self, seconds_per_batch):
+        import numpy as np
+        import oracle
+        from oracle import torch_path
+        self.np = np
+        self.oracle = oracle
+        self.tp = torch_path
+        self.cores = len(os.sched_getaffinity(0))
+        self.seconds = seconds_per_batch
+        self.checked = []
+
+    # -- the reference CPU path, timed --------------------------------------
+    def time_torch_path(self, B, resid_fmt=qpd.RESID_INT4, per_head=True):
+        """us per step of the torch restatement at batch B (HV=32, K=V=128,
+        fp32, the configs' input distributions), over about `seconds` of
+        steps after one untimed step; torch threads = this process's cores."""
+        prev = torch.get_num_threads()
+        torch.set_num_threads(self.cores)
+        try:
+            S = B + 1
+            g = torch.Generator().manual_seed(B)
+            h0 = torch.randn(S, HV, V, K, generator=g) * 0.1
+            sc, ss = (torch.from_numpy(x) for x in self.oracle.quantize_rows(h0.numpy()))
+            rc = torch.zeros(S, HV, V, K // 2 if resid_fmt == qpd.RESID_INT4 else K, dtype=torch.int8)
+            rs = torch.zeros((S, HV) if per_head else (S, HV, V))
+            sets, A_log, dt_bias = make_step_inputs(B, 2, "cpu", 5)
+            idx = torch.arange(1, S, dtype=torch.int32)
+
+            def step(t):
+                mixed, a, b = sets[t % 2]
+                self.tp.packed_decode_torch(mixed, a, b, A_log, dt_bias, 1.0, sc, ss, rc, rs, idx, H,
+                                            resid_fmt=resid_fmt, per_head=per_head)
+
+            step(0)
+            n = 0
+            t0 = time.perf_counter()
+            while True:
+                step(n)
+                n += 1
+                el = time.perf_counter() - t0
+                if el >= self.seconds or n >= 2000:
+                    break
+        finally:
+            torch.set_num_threads(prev)
+        us = el / n * 1e6
+        nb = algorithmic_bytes(B, H, HV, K, V, resid_fmt, per_head)
+        return {"us": round(us, 1), "GBps": round(nb / (us * 1e-6) / 1e9, 3), "steps": n, "seconds": round(el, 2)}
+
+    def time_c_oracle(self, B, resid_fmt=qpd.RESID_INT4, per_head=True, seconds=3.0):
+        """us per step of the C oracle (OpenMP over (request, head), every
+        core) on the same workload: a second CPU figure beside the torch path."""
+        np = self.np
+        S = B + 1
+        rng = np.random.default_rng(0)
+        h0 = (rng.standard_normal((S, HV, V, K)) * 0.1).astype(np.float32)
+        sc, ss = self.oracle.quantize_rows(h0)
+        rc = np.zeros((S, HV, V, K // 2 if resid_fmt == qpd.RESID_INT4 else K), np.int8)
+        rs = np.zeros((S, HV) if per_head else (S, HV, V), np.float32)
+        sets, A_log, dt_bias = make_step_inputs(B, 2, "cpu", 5)
+        idx = np.arange(1, S, dtype=np.int32)
+        n = 0
+        t0 = time.perf_counter()
+        while True:
+            mixed, a, b = sets[n % 2]
+            self.oracle.packed_decode(mixed.numpy(), a.numpy(), b.numpy(), A_log.numpy(), dt_bias.numpy(), 1.0,
+                                      sc, ss, rc, rs, idx, H, resid_fmt=resid_fmt, per_head=per_head,
+                                      nthreads=self.cores)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= seconds or n >= 2000:
+                break
+        return {"us": round(el / n * 1e6, 1), "steps": n, "threads": self.cores}
+
+    # -- checks of the GPU steps that are timed -------------------------------
+    def _record(self, name, ok, detail=""):
+        self.checked.append({"line": name, "ok": bool(ok), **({"detail": detail} if detail else {})})
+        if not ok:
+            raise RuntimeError(f"bench: the GPU result of {name} differs from the oracle ({detail})")
+        return True
+
+    @staticmethod
+    def _host(t):
+        return t.detach().float().cpu().numpy() if t.dtype in (torch.bfloat16, torch.float16) \
+            else t.detach().cpu().numpy().copy()
+
+    def check_packed_decode(self, name, run, pool, ids, inputs, out, resid_fmt, per_head, quant_mode="fast",
+                            l2norm=False, scale=1.0, bits=8, Hq=H):
+        """run() launches one GPU decode step that reads and writes the slots
+        `ids` of `pool` and writes `out`."""
+        np, orc = self.np, self.oracle
+        torch.cuda.synchronize()
+        li = ids.long()
+        live = li > 0
+        gather = li.clamp(min=0)
+        compact = [np.concatenate([np.zeros_like(self._host(x[:1])), self._host(x[gather])]) for x in pool]
+        run()
+        torch.cuda.synchronize()
+        B = ids.shape[0]
+        cidx = np.where(live.cpu().numpy(), np.arange(1, B + 1), 0).astype(np.int32)
+        mode = orc.MODE_EXACT if quant_mode == "exact" else orc.MODE_FAST
+        ref = orc.packed_decode(*(self._host(x).astype(np.float32) for x in inputs), scale, *compact, cidx, Hq,
+                                use_qk_l2norm=l2norm, resid_fmt=resid_fmt, per_head=per_head,
+                                state_bits=bits, mode=mode)
+        got = self._host(out)[:, 0]
+        if out.dtype == torch.bfloat16:
+            ref = orc.bf16_round(ref)
+        ok = np.array_equal(got, ref)
+        lv = live.cpu().numpy()
+        for x, c in zip(pool, compact):
+            ok = ok and np.array_equal(self._host(x[gather])[lv], c[1:][lv])
+        return self._record(name, ok, "" if ok else "outputs or state differ")
+
+    def check_quant_step(self, name, run, ins, outs, res_fmt, bits=8):
+        """statequant layout: ins = (h_int8, scale, e, e_scale, q, k, v, alpha,
+        beta), outs = (o, h_int8, scale, e, e_scale) written by run()."""
+        np, orc = self.np, self.oracle
+
+        def resid_store(t):   # the residual as the oracle stores it (fp16 / e5m2 as raw bits)
+            if res_fmt == sq.RES_FP16:
+                return t.detach().cpu().view(torch.int16).numpy().view(np.uint16)
+            if res_fmt == sq.RES_FP8:
+                return t.detach().cpu().view(torch.uint8).numpy()
+            return self._host(t)
+
+        torch.cuda.synchronize()
+        hin = [None if x is None else (resid_store(x) if i == 2 else self._host(x)) for i, x in enumerate(ins)]
+        run()
+        torch.cuda.synchronize()
+        ref = orc.quant_step_kv(hin[0], hin[1], hin[2], hin[3] if res_fmt == sq.RES_INT8 else None, *hin[4:],
+                                bits=bits, res_fmt=res_fmt)
+        ok = True
+        for i, (g, r) in enumerate(zip(outs, ref)):
+            if r is None:
+                continue
+            ok = ok and np.array_equal(resid_store(g) if i == 3 else self._host(g), r)
+        return self._record(name, ok, "" if ok else "statequant step differs")
+
+    def check_fp32_step(self, name, run, h, q, k, v, al, be, o, h_out):
+        np, orc = self.np, self.oracle
+        torch.cuda.synchronize()
+        hh = [self._host(x) for x in (h, q, k, v, al, be)]
+        run()
+        torch.cuda.synchronize()
+        h_ref, o_ref = orc.fp32_step_kv(*hh)
+        ok = np.array_equal(self._host(o), o_ref) and np.array_equal(self._host(h_out), h_ref)
+        return self._record(name, ok, "" if ok else "fp32 step differs")
+
+    def check_float_state(self, name, run, state, ids, inputs, out, Hq=H, l2norm=False, scale=1.0):
+        np, orc = self.np, self.oracle
+        torch.cuda.synchronize()
+        li = ids.long()
+        B = ids.shape[0]
+        compact = np.concatenate([np.zeros_like(self._host(state[:1])), self._host(state[li])]).astype(np.float32)
+        run()
+        torch.cuda.synchronize()
+        ref = orc.packed_decode_float_state(*(self._host(x).astype(np.float32) for x in inputs), scale, compact,
+                                            np.arange(1, B + 1, dtype=np.int32), Hq,
+                                            bf16=state.dtype == torch.bfloat16, use_qk_l2norm=l2norm)
+        ok = np.array_equal(self._host(out)[:, 0], ref) and np.array_equal(self._host(state[li]), compact[1:])
+        return self._record(name, ok, "" if ok else "float-state step differs")
+
+    def check_quantize_rows(self, name, run, x, codes, scale, qmax=127.0, rows=4096):
+        np, orc = self.np, self.oracle
+        run()
+        torch.cuda.synchronize()
+        xk = self._host(x.reshape(-1, x.shape[-1])[:rows])
+        c_ref, s_ref = orc.quantize_rows(xk, qmax)
+        ok = np.array_equal(self._host(codes.reshape(-1, x.shape[-1])[:rows]), c_ref) and \
+            np.array_equal(self._host(scale.reshape(-1)[:rows]), s_ref)
+        return self._record(name, ok, "" if ok else "row ingest differs")
+
+    def check_quantize_cols(self, name, run, x, codes, scale, qmax=127.0, mats=8):
+        np, orc = self.np, self.oracle
+        run()
+        torch.cuda.synchronize()
+        Kx, Vx = x.shape[-2:]
+        xk = self._host(x.reshape(-1, Kx, Vx)[:mats])
+        c_ref, s_ref = orc.quantize_cols(xk, qmax)
+        ok = np.array_equal(self._host(codes.reshape(-1, Kx, Vx)[:mats]), c_ref) and \
+            np.array_equal(self._host(scale.reshape(-1, Vx)[:mats]), s_ref)
+        return self._record(name, ok, "" if ok else "column ingest differs")
 
 
 class Timer:
@@ -163,11 +326,62 @@ class Timer:
         return self.s.elapsed_time(self.e)
 
 
+def _capture(device, step, ts):
+    """One HIP graph holding step(t) for t in ts, captured on a side stream."""
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            for t in ts:
+                step(t)
+    torch.cuda.current_stream(device).wait_stream(side)
+    torch.cuda.synchronize()
+    return graph
+
+
+class StepReplayer:
+    """Replays exactly n launches of step(t): n // period replays of a graph
+    of steps 0 .. period-1, then one graph of the first n % period steps."""
+
+    def __init__(self, device, step, period):
+        self.device, self.step, self.period = device, step, period
+        self.full = _capture(device, step, range(period))
+        self.tails = {}
+
+    def replay(self, n):
+        for _ in range(n // self.period):
+            self.full.replay()
+        r = n % self.period
+        if r:
+            if r not in self.tails:
+                self.tails[r] = _capture(self.device, self.step, range(r))
+            self.tails[r].replay()
+
+    def time_ms_per_step(self, steps, warmup):
+        """Exactly `warmup` untimed steps, then exactly `steps` steps between
+        two HIP events on the launch stream, synchronised on both sides."""
+        if steps % self.period:
+            self.replay(steps % self.period)   # capture the remainder graph outside the timed region
+        self.replay(warmup)
+        torch.cuda.synchronize()
+        timer = Timer(self.device)
+        timer.start()
+        self.replay(steps)
+        ms = timer.stop_ms() / steps
+        torch.cuda.synchronize()
+        return ms
+
+
 def run_config(device, B, resid_fmt, per_head, steps, warmup, groups, quant_mode="fast", seed=0,
-               act_dtype=torch.float32):
-    """Returns (device ms per step from a replayed graph, host-inclusive ms per
-    eager call). The graph holds one step per slot group. `act_dtype` is the
-    dtype of mixed_qkv, a, b and out (vLLM runs bf16 activations)."""
+               act_dtype=torch.float32, cpu=None, name=None):
+    """One configuration of the decode step: a pool of B * groups + 1 slots
+    (state from 64 fp32 warm-up steps), each step on the next group of B
+    random slots. Returns {ms: device ms per step over exactly `steps`
+    graph-replayed steps, host_ms: host-inclusive ms per eager call,
+    validated: the CPU leg's bit-exact check of one step of this very
+    configuration (None without a CPU leg)}. `act_dtype` is the dtype of
+    mixed_qkv, a, b and out (vLLM runs bf16 activations)."""
     S = B * groups + 1
     state = warm_state(S, device, seed)
     pool = qpd.init_quantized_state(S, HV, V, K, device, h0=state, resid_fmt=resid_fmt,
@@ -186,6 +400,12 @@ def run_config(device, B, resid_fmt, per_head, steps, warmup, groups, quant_mode
             mixed, a, b, A_log, dt_bias, 1.0, *pool, out, idx_groups[t % groups],
             resid_fmt=resid_fmt, quant_mode=quant_mode)
 
+    validated = None
+    if cpu is not None:
+        mixed, a, b = sets[0]
+        validated = cpu.check_packed_decode(name or f"B{B}", lambda: step(0), pool, idx_groups[0],
+                                            (mixed, a, b, A_log, dt_bias), out, resid_fmt, per_head, quant_mode)
+
     # eager calls: host-inclusive latency per call
     for t in range(min(warmup, 50)):
         step(t)
@@ -197,32 +417,13 @@ def run_config(device, B, resid_fmt, per_head, steps, warmup, groups, quant_mode
     torch.cuda.synchronize()
     host_ms = (time.perf_counter() - t0) * 1e3 / n_eager
 
-    # graph of `groups` consecutive steps, replayed
-    side = torch.cuda.Stream(device)
-    side.wait_stream(torch.cuda.current_stream(device))
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(side):
-        with torch.cuda.graph(graph, stream=side):
-            for t in range(groups):
-                step(t)
-    torch.cuda.current_stream(device).wait_stream(side)
-    torch.cuda.synchronize()
-    reps_w = max(1, -(-warmup // groups))
-    reps = max(1, -(-steps // groups))
-    for _ in range(reps_w):
-        graph.replay()
-    torch.cuda.synchronize()
-    timer = Timer(device)
-    timer.start()
-    for _ in range(reps):
-        graph.replay()
-    ms = timer.stop_ms() / (reps * groups)
-    torch.cuda.synchronize()
-    if not torch.isfinite(out).all():
+    rep = StepReplayer(device, step, groups)
+    ms = rep.time_ms_per_step(steps, warmup)
+    if not torch.isfinite(out.float()).all():
         raise RuntimeError("non-finite output in the timed run")
-    del graph, pool
+    del rep, pool
     torch.cuda.empty_cache()
-    return ms, host_ms
+    return {"ms": ms, "host_ms": host_ms, "validated": validated}
 
 
 def _graph_time(device, step, n_steps, warmup, reps_cap=None):
@@ -256,7 +457,7 @@ def _graph_time(device, step, n_steps, warmup, reps_cap=None):
     return sorted(trials)[1]
 
 
-def multilayer_token(device, layers=24, B=64, live=None, tokens=20, seed=7):
+def multilayer_token(device, layers=24, B=64, live=None, tokens=20, seed=7, cpu=None):
     """Config C5's decode shape as a serving engine runs it: one token through
     `layers` GDN layers at batch B (int4 residual, per-head scale), each layer
     with its own pool, called eagerly (host-inclusive time per token: one
@@ -279,6 +480,13 @@ def multilayer_token(device, layers=24, B=64, live=None, tokens=20, seed=7):
             qpd.quantized_gated_delta_rule_packed_decode(mixed, a, b, A_log, dt_bias, 1.0, *pools[layer],
                                                          outs[layer], idx, resid_fmt=qpd.RESID_INT4)
 
+    validated = None
+    if cpu is not None:   # layer 0's step of this shape, NULL padding included
+        validated = cpu.check_packed_decode(
+            f"multilayer_c5_live{live}",
+            lambda: qpd.quantized_gated_delta_rule_packed_decode(mixed, a, b, A_log, dt_bias, 1.0, *pools[0],
+                                                                 outs[0], idx, resid_fmt=qpd.RESID_INT4),
+            pools[0], idx, (mixed, a, b, A_log, dt_bias), outs[0], qpd.RESID_INT4, True)
     for _ in range(3):
         token()
     torch.cuda.synchronize()
@@ -294,12 +502,12 @@ def multilayer_token(device, layers=24, B=64, live=None, tokens=20, seed=7):
     return {"layers": layers, "batch": B, "live_requests": live,
             "eager_host_us_per_token": round(eager_ms * 1e3, 2),
             "graph_us_per_token": round(graph_ms * 1e3, 2),
-            "graph_us_per_layer": round(graph_ms * 1e3 / layers, 3),
+            "graph_us_per_layer": round(graph_ms * 1e3 / layers, 3), "validated": validated,
             "GBps": round(nb / (graph_ms * 1e-3) / 1e9, 1),
             "frac": round(nb / (graph_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
 
 
-def ingest_arm(device, slots=257):
+def ingest_arm(device, slots=257, cpu=None):
     """State ingest (init_quantized_state's quantization, ck_quantize_rows) of a
     [slots, HV, V, K] prefill state in fp32 and bf16: reads the state, writes
     int8 codes and one fp32 scale per row. Buffers rotate over > 256 MB."""
@@ -317,10 +525,11 @@ def ingest_arm(device, slots=257):
             _native.check(L.ck_quantize_rows(x.data_ptr(), code, K, rows, K, 127.0, codes.data_ptr(),
                                              scale.data_ptr(), _native.stream_handle(device)), "ck_quantize_rows")
 
+        validated = cpu.check_quantize_rows(name, lambda: step(0), x, codes, scale) if cpu else None
         ms = _graph_time(device, step, 1, 20, 20)
         nb = rows * K * (esz + 1) + rows * 4
         res[name] = {"us": round(ms * 1e3, 2), "bytes": nb, "GBps": round(nb / (ms * 1e-3) / 1e9, 1),
-                     "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+                     "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "validated": validated}
         del x, codes, scale
         torch.cuda.empty_cache()
     # the statequant layout's per-V-column quantization (per_v_channel_quantize,
@@ -333,10 +542,11 @@ def ingest_arm(device, slots=257):
         _native.check(L.ck_quantize_cols(x.data_ptr(), slots * HV, K, V, 127.0, codes.data_ptr(), scale.data_ptr(),
                                          _native.stream_handle(device)), "ck_quantize_cols")
 
+    validated = cpu.check_quantize_cols("ingest_cols_fp32", lambda: cstep(0), x, codes, scale) if cpu else None
     ms = _graph_time(device, cstep, 1, 20, 20)
     nb = slots * HV * K * V * 5 + slots * HV * V * 4
     res["ingest_cols_fp32"] = {"us": round(ms * 1e3, 2), "bytes": nb, "GBps": round(nb / (ms * 1e-3) / 1e9, 1),
-                               "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+                               "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "validated": validated}
     del x, codes, scale
     torch.cuda.empty_cache()
     return res
@@ -360,14 +570,26 @@ def slot_ops_arm(device, n=256):
     def reset_step(t):
         qpd.reset_quantized_state(pool, groups[t % 4])
 
+    # each operation checked once on these buffers, byte for byte against
+    # torch's own gather of the same slots (random pool contents first)
+    for t in pool:
+        t.copy_(torch.randint(-100, 100, t.shape, device=device).to(t.dtype))
+    src_before = [t[groups[0].long()].clone() for t in pool]
+    copy_step(0)
+    ok_copy = all(torch.equal(t[groups[1].long()], b) for t, b in zip(pool, src_before))
+    reset_step(1)
+    ok_reset = all(bool((t[groups[1].long()] == 0).all()) for t in pool)
+    del src_before
+    if not (ok_copy and ok_reset):
+        raise RuntimeError("bench: slot copy / reset moved the wrong bytes")
     ms = _graph_time(device, copy_step, 3, 20, 20)
     nb = 2 * n * slot_bytes
     res["pool_copy_slots"] = {"us": round(ms * 1e3, 2), "bytes": nb, "GBps": round(nb / (ms * 1e-3) / 1e9, 1),
-                              "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+                              "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "validated": ok_copy}
     ms = _graph_time(device, reset_step, 4, 20, 20)
     nb = n * slot_bytes
     res["pool_reset_slots"] = {"us": round(ms * 1e3, 2), "bytes": nb, "GBps": round(nb / (ms * 1e-3) / 1e9, 1),
-                               "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+                               "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "validated": ok_reset}
     del pool
     torch.cuda.empty_cache()
     return res
@@ -383,7 +605,7 @@ def statequant_bytes(B, HV, K, V, res_fmt):
     return B * HV * per
 
 
-def arms(device, batches=(8, 64), steps=800):
+def arms(device, batches=(8, 64), steps=800, cpu=None):
     """The other entry points at config shapes (HV=32, K=V=128, fp32
     activations): the statequant-layout step for each residual format, its fp32
     baseline, and the unquantized fp32 / bf16 state arms of the vLLM-layout
@@ -394,9 +616,9 @@ def arms(device, batches=(8, 64), steps=800):
     res = {}
     gen = torch.Generator(device=device).manual_seed(3)
 
-    def rec(name, ms, nbytes):
+    def rec(name, ms, nbytes, validated=None):
         res[name] = {"us": round(ms * 1e3, 3), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
-                     "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+                     "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "validated": validated}
 
     for B in batches:
         q = torch.randn(B, HV, K, device=device, generator=gen)
@@ -425,8 +647,14 @@ def arms(device, batches=(8, 64), steps=800):
                                          b_[3].data_ptr(), B, HV, K, V, 127.0, res_fmt, 0,
                                          _native.stream_handle(device))
                 _native.check(st, "statequant step")
+            name = f"statequant_B{B}_{sq.residual_label(res_fmt)}"
+            validated = None
+            if cpu is not None:
+                a_, b_ = sets[0], sets[1]
+                validated = cpu.check_quant_step(name, lambda: step(0), (*a_, q, k, v, al, be),
+                                                 (o, *b_), res_fmt)
             ms = _graph_time(device, step, nsets, -(-200 // nsets), max(2, steps // nsets))
-            rec(f"statequant_B{B}_{sq.residual_label(res_fmt)}", ms, statequant_bytes(B, HV, K, V, res_fmt))
+            rec(name, ms, statequant_bytes(B, HV, K, V, res_fmt), validated)
             del sets
         # fp32 baseline step, ping-pong between state buffers
         nsets = max(2, min(64, -(-(512 << 20) // (B * HV * K * V * 4))))
@@ -437,8 +665,10 @@ def arms(device, batches=(8, 64), steps=800):
                                     al.data_ptr(), be.data_ptr(), o.data_ptr(), hsets[(t + 1) % nsets].data_ptr(),
                                     B, HV, K, V, _native.stream_handle(device))
             _native.check(st, "fp32 step")
+        validated = cpu.check_fp32_step(f"fp32_step_B{B}", lambda: fstep(0), hsets[0], q, k, v, al, be, o,
+                                        hsets[1]) if cpu else None
         ms = _graph_time(device, fstep, nsets, -(-200 // nsets), max(2, steps // nsets))
-        rec(f"fp32_step_B{B}", ms, B * HV * (2 * 4 * K * V + 2 * 4 * K + 2 * 4 * V + 8))
+        rec(f"fp32_step_B{B}", ms, B * HV * (2 * 4 * K * V + 2 * 4 * K + 2 * 4 * V + 8), validated)
         del hsets
         torch.cuda.empty_cache()
     # vLLM-layout unquantized arms at B=64 (in place, slot groups rotated)
@@ -459,8 +689,13 @@ def arms(device, batches=(8, 64), steps=800):
                 0 if dtype == torch.float32 else 1, state.stride(0), out.data_ptr(), 0,
                 idxs[t % len(idxs)].data_ptr(), 1, S, B, H, HV, K, V, 0, _native.stream_handle(device))
             _native.check(st, "float-state step")
+        validated = None
+        if cpu is not None:
+            mixed, a, b = sets_in[0]
+            validated = cpu.check_float_state(f"vllm_{name}_state_B{B}", lambda: vstep(0), state, idxs[0],
+                                              (mixed, a, b, A_log, dt_bias), out)
         ms = _graph_time(device, vstep, groups, -(-200 // groups), max(2, steps // groups))
-        rec(f"vllm_{name}_state_B{B}", ms, float_state_bytes(B, H, HV, K, V, esz))
+        rec(f"vllm_{name}_state_B{B}", ms, float_state_bytes(B, H, HV, K, V, esz), validated)
         del state
         torch.cuda.empty_cache()
     return res
@@ -513,14 +748,22 @@ def hbm_copy_peak(device, total_bytes, pool_bytes=1 << 31, grids=(512, 2048, 409
 
 
 def float_state_step(state, mixed, a, b, A_log, dt_bias, scale, out, idx, l2norm):
-    """One step of the unquantized fp32 state arm (ck_gdn_packed_decode_float_state)."""
+    """One step of the unquantized state arm (ck_gdn_packed_decode_float_state)
+    on an fp32 or bf16 state pool; every tensor's dtype code is its own (the
+    kernel addresses the pool by the state dtype it is given)."""
     from carrykernel_amd import _native
+    if state.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"the state arm takes a float32 or bfloat16 pool, got {state.dtype}")
+    for t, nm in ((mixed, "mixed_qkv"), (a, "a"), (b, "b"), (A_log, "A_log"), (dt_bias, "dt_bias"), (out, "out")):
+        _native.dtype_code(t, nm)
     S, hv, v, k = state.shape
+    dc = _native.dtype_code
     st = _native.lib().ck_gdn_packed_decode_float_state(
-        mixed.data_ptr(), 0, mixed.stride(0), a.data_ptr(), 0, a.stride(0), b.data_ptr(), 0, b.stride(0),
-        A_log.data_ptr(), 0, dt_bias.data_ptr(), 0, float(scale), state.data_ptr(), 0, state.stride(0),
-        out.data_ptr(), 0, idx.data_ptr(), idx.stride(0), S, mixed.shape[0], (mixed.shape[1] - hv * v) // (2 * k),
-        hv, k, v, int(l2norm),
+        mixed.data_ptr(), dc(mixed, "mixed_qkv"), mixed.stride(0), a.data_ptr(), dc(a, "a"), a.stride(0),
+        b.data_ptr(), dc(b, "b"), b.stride(0), A_log.data_ptr(), dc(A_log, "A_log"), dt_bias.data_ptr(),
+        dc(dt_bias, "dt_bias"), float(scale), state.data_ptr(), dc(state, "state"), state.stride(0),
+        out.data_ptr(), dc(out, "out"), idx.data_ptr(), idx.stride(0), S, mixed.shape[0],
+        (mixed.shape[1] - hv * v) // (2 * k), hv, k, v, int(l2norm),
         _native.stream_handle(state.device))
     _native.check(st, "float-state step")
 
@@ -695,14 +938,16 @@ def main():
     ap.add_argument("--sweep", action="store_true",
                     help="time every B in {1, 8, 64, 256} x residual format x scale granularity (default: "
                          "the headline format at B in {1, 8, 64, 256} and the C2 / C4 steps)")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-cpu", action="store_true",
+                    help="skip the CPU leg (the reference CPU path timing and the oracle checks of each line)")
     ap.add_argument("--no-sweep", action="store_true",
                     help="time only the headline configuration (no batch sweep, no other entry points)")
     ap.add_argument("--drift", action="store_true",
                     help="instead: config C5 drift (24 layers x B=64 x 2048 tokens, int8 and int6 state) "
                          "against the fp32 state arm; prints one JSON line")
     ap.add_argument("--drift-tokens", type=int, default=2048)
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=4.0,
+                    help="seconds of CPU-path steps timed per batch in the CPU leg")
     ap.add_argument("--timeline", action="store_true",
                     help="instead: per-workgroup timeline of one launch of the chosen step from the "
                          "timestamped measurement build (prints one JSON line)")
@@ -740,8 +985,10 @@ def main():
         print(json.dumps(timeline_report(device, B, resid_fmt, per_head, max(2, min(64, 1024 // B)))), flush=True)
         return
 
-    ms, host_ms = run_config(device, B, resid_fmt, per_head, args.steps, args.warmup, args.groups,
-                             args.quant_mode)
+    cpu = None if args.no_cpu else CpuLeg(args.cpu_seconds)
+    r = run_config(device, B, resid_fmt, per_head, args.steps, args.warmup, args.groups, args.quant_mode,
+                   cpu=cpu, name=f"B{B}_{args.resid}_{args.rscale}_{args.quant_mode}")
+    ms, host_ms = r["ms"], r["host_ms"]
     nbytes = algorithmic_bytes(B, H, HV, K, V, resid_fmt, per_head)
     gbps = nbytes / (ms * 1e-3) / 1e9
     line = {
@@ -764,6 +1011,7 @@ def main():
                    "batch": B, "value_heads": HV, "qk_heads": H, "K": K, "V": V,
                    "resid": args.resid, "resid_scale": args.rscale, "quant_mode": args.quant_mode,
                    "pool_slots": B * args.groups + 1},
+        "validated": r["validated"],
         "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
                      "bytes_per_launch": nbytes},
@@ -773,46 +1021,59 @@ def main():
     if os.path.exists(traffic_path):
         with open(traffic_path) as f:
             line["roofline"]["traffic"] = json.load(f).get("traffic_bytes_per_launch")
-    # batch sweep of the same format (config C3), plus config C2's (B=8, int8
-    # residual, per-head scale) and C4's (B=128, int4, per-row scale) steps;
-    # --sweep adds every batch x residual format x scale granularity
+    # batch sweep of the same format (config C3) in both arithmetic modes at
+    # B = 64 and 256, plus config C2's (B=8, int8 residual, per-head scale)
+    # and C4's (B=128, int4, per-row scale) steps; --sweep adds every batch x
+    # residual format x scale granularity. Every entry is checked by the CPU
+    # leg before it is timed, and the C3 batches carry the reference CPU
+    # path's time at the same batch.
     formats = {"int4_head": (qpd.RESID_INT4, True), "int4_row": (qpd.RESID_INT4, False),
                "int8_head": (qpd.RESID_INT8, True), "int8_row": (qpd.RESID_INT8, False)}
     if args.no_sweep:
         cases = []
     elif args.sweep:
-        cases = [(bb, f) for bb in (1, 8, 64, 256) for f in formats] + [(128, "int4_row")]
+        cases = [(bb, f, "fast") for bb in (1, 8, 64, 256) for f in formats] + [(128, "int4_row", "fast")]
     else:
-        cases = [(bb, "int4_head") for bb in (1, 8, 256)] + [(8, "int8_head"), (128, "int4_row")]
+        cases = [(bb, "int4_head", "fast") for bb in (1, 8, 256)] + [(8, "int8_head", "fast"),
+                                                                      (128, "int4_row", "fast")]
+    if not args.no_sweep:
+        cases += [(64, "int4_head", "exact"), (256, "int4_head", "exact")]
     sweep = {}
+
+    def key(bb, fmt_name, mode):
+        return f"B{bb}_{fmt_name}" + ("" if mode == "fast" else "_exact")
+
     if args.batch == 64 and args.resid == "int4" and args.rscale == "head":
-        sweep["B64_int4_head"] = {"us": line["us_per_step"], "host_us": line["host_us_per_eager_call"],
-                                  "GBps": line["value"], "frac": line["roofline"]["frac"]}
-    for bb, fmt_name in cases:
-        if f"B{bb}_{fmt_name}" in sweep:
+        sweep[key(64, "int4_head", args.quant_mode)] = {
+            "us": line["us_per_step"], "host_us": line["host_us_per_eager_call"], "GBps": line["value"],
+            "frac": line["roofline"]["frac"], "validated": r["validated"]}
+    for bb, fmt_name, mode in cases:
+        if key(bb, fmt_name, mode) in sweep:
             continue
         fmt, ph = formats[fmt_name]
         groups = max(2, min(64, 1024 // bb))
-        m, hm = run_config(device, bb, fmt, ph, args.steps, args.warmup, groups, args.quant_mode)
+        rr = run_config(device, bb, fmt, ph, args.steps, args.warmup, groups, mode, cpu=cpu,
+                        name=key(bb, fmt_name, mode))
         nb = algorithmic_bytes(bb, H, HV, K, V, fmt, ph)
-        sweep[f"B{bb}_{fmt_name}"] = {"us": round(m * 1e3, 3), "host_us": round(hm * 1e3, 3),
-                                     "GBps": round(nb / (m * 1e-3) / 1e9, 1),
-                                     "frac": round(nb / (m * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+        sweep[key(bb, fmt_name, mode)] = {"us": round(rr["ms"] * 1e3, 3), "host_us": round(rr["host_ms"] * 1e3, 3),
+                                          "GBps": round(nb / (rr["ms"] * 1e-3) / 1e9, 1),
+                                          "frac": round(nb / (rr["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                                          "validated": rr["validated"]}
     if not args.no_sweep:   # the headline step with vLLM's bf16 activations and output
-        m, hm = run_config(device, 64, qpd.RESID_INT4, True, args.steps, args.warmup, 16, args.quant_mode,
-                           act_dtype=torch.bfloat16)
+        rr = run_config(device, 64, qpd.RESID_INT4, True, args.steps, args.warmup, 16, args.quant_mode,
+                        act_dtype=torch.bfloat16, cpu=cpu, name="B64_int4_head_bf16act")
         nb = algorithmic_bytes(64, H, HV, K, V, qpd.RESID_INT4, True, act_bytes=2)
-        sweep["B64_int4_head_bf16act"] = {"us": round(m * 1e3, 3), "host_us": round(hm * 1e3, 3),
-                                          "GBps": round(nb / (m * 1e-3) / 1e9, 1),
-                                          "frac": round(nb / (m * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
-    line["sweep"] = dict(sorted(sweep.items(), key=lambda kv: (int(kv[0][1:kv[0].index("_")]), kv[0])))
+        sweep["B64_int4_head_bf16act"] = {"us": round(rr["ms"] * 1e3, 3), "host_us": round(rr["host_ms"] * 1e3, 3),
+                                          "GBps": round(nb / (rr["ms"] * 1e-3) / 1e9, 1),
+                                          "frac": round(nb / (rr["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                                          "validated": rr["validated"]}
     if not args.no_sweep:
         # the C5 shape through 24 layers per token: eager vs one graph per token,
         # full and NULL-padded (48 live requests in a batch-64 capture)
-        line["multilayer_c5"] = {"full": multilayer_token(device),
-                                 "padded": multilayer_token(device, live=48)}
-        line["arms"] = arms(device)
-        line["arms"].update(ingest_arm(device))
+        line["multilayer_c5"] = {"full": multilayer_token(device, cpu=cpu),
+                                 "padded": multilayer_token(device, live=48, cpu=cpu)}
+        line["arms"] = arms(device, cpu=cpu)
+        line["arms"].update(ingest_arm(device, cpu=cpu))
         line["arms"].update(slot_ops_arm(device))
         # measured copy ceiling at the headline's byte count and for a 1 GiB copy
         at = hbm_copy_peak(device, nbytes)
@@ -821,8 +1082,30 @@ def main():
                              "at_workload_bytes": at, "large": big,
                              "frac_of_copy_at_workload": round(gbps / at["GBps"], 4),
                              "frac_of_copy_large": round(gbps / big["GBps"], 4)}
-    if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(B, resid_fmt, per_head, args.cpu_seconds)
+    if cpu is not None:
+        # the reference CPU path at every C3 batch the sweep times (and the
+        # headline's), on this host's cores; bytes per step as on the GPU
+        by_batch = {}
+        for bb in sorted({B} | ({1, 8, 64, 256} if not args.no_sweep else set())):
+            by_batch[bb] = cpu.time_torch_path(bb, resid_fmt if bb == B else qpd.RESID_INT4,
+                                               per_head if bb == B else True)
+            k_ = key(bb, "int4_head", "fast")
+            if k_ in sweep:
+                sweep[k_]["cpu_us"] = by_batch[bb]["us"]
+                sweep[k_]["gpu_vs_cpu"] = round(by_batch[bb]["us"] / sweep[k_]["us"], 1)
+        head = by_batch[B]
+        line["cpu_baseline"] = {
+            "value": head["GBps"], "unit": "GB/s", "us_per_step": head["us"],
+            "cores": cpu.cores, "threads": cpu.cores, "kind": "port",
+            "sample": (f"{head['steps']} steps of the B={B} workload ({head['seconds']} s) through "
+                       "oracle/torch_path.py, a torch restatement of the reference CPU path "
+                       "(statequant/kernel.py:149-178) in the vLLM layout, torch threads = "
+                       f"{cpu.cores} = the cores this process may run on"),
+            "by_batch": {str(bb): v for bb, v in by_batch.items()},
+            "c_oracle_us_per_step": cpu.time_c_oracle(B, resid_fmt, per_head),
+            "validated_lines": len(cpu.checked),
+        }
+    line["sweep"] = dict(sorted(sweep.items(), key=lambda kv: (int(kv[0][1:kv[0].index("_")]), kv[0])))
     print(json.dumps(line), flush=True)
 
 

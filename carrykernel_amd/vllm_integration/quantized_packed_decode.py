@@ -376,13 +376,19 @@ def init_quantized_state(num_slots: int, HV: int, V: int, K: int, device,
     """Allocate the quantized state pool, optionally seeding slot contents.
 
     quantized_packed_decode.py:330-352. ``h0``, when given, is
-    ``[num_slots, HV, V, K]`` (fp32 / bf16 / fp16) and is quantized into the
-    pool on the GPU (``ck_quantize_rows``: scale = max(amax_K, eps) / qmax,
+    ``[num_slots, HV, V, K]`` in any floating dtype on any device (float64 is
+    read as fp32, a host tensor is copied to ``device``) and is quantized into
+    the pool on the GPU (``ck_quantize_rows``: scale = max(amax_K, eps) / qmax,
     codes = rne(h0 / scale)); the residual starts at zero. Returns
     ``(state_codes, state_scale, resid_codes, resid_scale)``.
     ``per_head_resid_scale`` allocates ``resid_scale`` as ``[num_slots, HV]``.
     """
     device = torch.device(device)
+    if h0 is not None:
+        if tuple(h0.shape) != (num_slots, HV, V, K):
+            raise ValueError(f"h0 must be {(num_slots, HV, V, K)}, got {tuple(h0.shape)}")
+        if not h0.is_floating_point():
+            raise ValueError(f"h0 must be a floating-point tensor, got {h0.dtype}")
     if device.type != "cuda":
         raise _native.HipUnavailable(f"the quantized pool lives on a GPU, got device {device}")
     resid_k = K // 2 if resid_fmt == RESID_INT4 else K
@@ -393,9 +399,12 @@ def init_quantized_state(num_slots: int, HV: int, V: int, K: int, device,
     resid_scale = torch.zeros(rs_shape, dtype=torch.float32, device=device)
 
     if h0 is not None:
-        if tuple(h0.shape) != (num_slots, HV, V, K):
-            raise ValueError(f"h0 must be {(num_slots, HV, V, K)}, got {tuple(h0.shape)}")
-        _native.require_gpu(h0, "h0")
+        # h0 may come from any device and in any float dtype, as the
+        # reference's (quantized_packed_decode.py:347-351 quantizes in h0's
+        # precision and copy_()s into the pool): move it to the pool's GPU,
+        # and narrow dtypes the kernel does not read (float64) to fp32.
+        if h0.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+            h0 = h0.to(torch.float32)
         h0 = h0.to(device).contiguous()
         qmax = float(2 ** (int(state_bits) - 1) - 1)
         L = _native.lib()

@@ -83,6 +83,7 @@ def lib():
             L.orc_f32_to_e5m2_n.argtypes = [_f32p, _u8p, _i64]
             L.orc_e5m2_to_f32_n.argtypes = [_u8p, _f32p, _i64]
             L.orc_quantize_cols.argtypes = [_f32p, _i64, _int, _int, _flt, _i8p, _f32p]
+            L.orc_bf16_round_n.argtypes = [_f32p, _f32p, _i64]
             L.orc_count_div_small_int_mismatches.restype = _i64
             L.orc_count_div_small_int_mismatches.argtypes = [_flt, _int, _int]
             _lib = L
@@ -306,10 +307,20 @@ def unpack_int4(packed: np.ndarray) -> np.ndarray:
 
 
 def bf16_round(x: np.ndarray) -> np.ndarray:
-    """fp32 -> bf16 (round to nearest even) -> fp32."""
-    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    """fp32 -> bf16 (round to nearest even) -> fp32; NaN stays NaN."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
     u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16 << 16
-    return (u & 0xFFFFFFFF).astype(np.uint32).view(np.float32)
+    r = (u & 0xFFFFFFFF).astype(np.uint32).view(np.float32)
+    return np.where(np.isnan(x), x, r)
+
+
+def bf16_round_c(x: np.ndarray) -> np.ndarray:
+    """The C oracle's bf16 rounding (bf16_round_f in gdn_oracle.c)."""
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().orc_bf16_round_n(x.ravel(), y.ravel(), x.size)
+    return y
 
 
 def gdn_step_f64(h, q, k, v, alpha, beta):

@@ -589,6 +589,11 @@ static float bf16_round_f(float x) {
   return orc_bits_to_float(u & 0xffff0000u);
 }
 
+/* bf16_round_f over an array (exported so tests can pin it against torch). */
+void orc_bf16_round_n(const float* x, float* y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) y[i] = bf16_round_f(x[i]);
+}
+
 int orc_packed_decode_float_state(const float* mixed, int64_t stride_mixed,
                                   const float* a, int64_t stride_a, const float* b, int64_t stride_b,
                                   const float* A_log, const float* dt_bias, float scale,

@@ -258,3 +258,51 @@ def test_bench_refuses_more_than_one_gpu():
                        text=True, timeout=300)
     assert r.returncode == 2
     assert "only --gpus 1" in r.stderr and r.stdout == ""
+
+
+def test_init_quantized_state_checks_h0_before_allocating():
+    """init_quantized_state rejects an h0 of the wrong shape or a non-float
+    dtype with ValueError before it touches a device; a float h0 on the host
+    is accepted (it is copied to the pool's GPU, which this host lacks)."""
+    from carrykernel_amd import _native
+    from carrykernel_amd.vllm_integration import quantized_packed_decode as qpd
+    with pytest.raises(ValueError, match="h0 must be"):
+        qpd.init_quantized_state(2, 1, 16, 16, "cuda", h0=torch.zeros(2, 1, 16, 8))
+    with pytest.raises(ValueError, match="floating-point"):
+        qpd.init_quantized_state(2, 1, 16, 16, "cuda", h0=torch.zeros(2, 1, 16, 16, dtype=torch.int32))
+    with pytest.raises(_native.HipUnavailable):
+        qpd.init_quantized_state(2, 1, 16, 16, "cpu", h0=torch.zeros(2, 1, 16, 16, dtype=torch.float64))
+
+
+def test_bench_float_state_step_passes_each_dtype_code(monkeypatch):
+    """bench.float_state_step hands the state arm the pool's own dtype code
+    (a bf16 pool addressed as fp32 would be read and written at twice its
+    size), and refuses pools of other dtypes before any call."""
+    import bench
+    calls = []
+
+    class FakeLib:
+        def ck_gdn_packed_decode_float_state(self, *args):
+            calls.append(args)
+            return 0
+
+    monkeypatch.setattr(_native, "lib", lambda: FakeLib())
+    monkeypatch.setattr(_native, "stream_handle", lambda dev: None)
+    B, H_, HV_, K_, V_ = 2, 1, 2, 16, 16
+    mixed = torch.zeros(B, 2 * H_ * K_ + HV_ * V_, dtype=torch.bfloat16)
+    a = torch.zeros(B, HV_)
+    b = torch.zeros(B, HV_, dtype=torch.float16)
+    A_log = torch.zeros(HV_)
+    dt = torch.zeros(HV_)
+    out = torch.zeros(B, 1, HV_, V_)
+    idx = torch.tensor([1, 2], dtype=torch.int32)
+    for sdt, code in ((torch.float32, 0), (torch.bfloat16, 1)):
+        state = torch.zeros(3, HV_, V_, K_, dtype=sdt)
+        bench.float_state_step(state, mixed, a, b, A_log, dt, 1.0, out, idx, False)
+        args = calls[-1]
+        assert args[15] == code                        # state dtype
+        assert (args[1], args[4], args[7], args[10], args[12], args[18]) == (1, 0, 2, 0, 0, 0)
+    with pytest.raises(ValueError, match="float32 or bfloat16"):
+        bench.float_state_step(torch.zeros(3, HV_, V_, K_, dtype=torch.float16), mixed, a, b, A_log, dt, 1.0,
+                               out, idx, False)
+    assert len(calls) == 2

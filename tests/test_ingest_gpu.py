@@ -92,3 +92,22 @@ def test_quantize_rows_padded_and_unaligned_rows(device, offset, rows=37, K=128)
     c_ref, s_ref = oracle.quantize_rows(np.ascontiguousarray(x[:, :K].cpu().numpy()), 127.0)
     np.testing.assert_array_equal(codes.cpu().numpy(), c_ref)
     np.testing.assert_array_equal(scale.cpu().numpy(), s_ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.bfloat16])
+def test_init_from_host_and_float64_prefill_state(device, dtype, S=3, HV=2, V=16, K=128):
+    """An h0 on the host, or in float64, seeds the pool like the same values
+    given on the GPU in fp32 (float64 is read as fp32; the reference accepts
+    any device and float dtype, quantized_packed_decode.py:347-351)."""
+    g = torch.Generator().manual_seed(7)
+    h0 = (torch.randn(S, HV, V, K, generator=g, dtype=torch.float64) * 0.2).to(dtype)
+    print(f"case ingest host h0 {dtype}", flush=True)
+    a = qpd.init_quantized_state(S, HV, V, K, device, h0=h0, resid_fmt=qpd.RESID_INT4)
+    ref_dtype = torch.float32 if dtype == torch.float64 else dtype
+    b = qpd.init_quantized_state(S, HV, V, K, device, h0=h0.to(ref_dtype).to(device), resid_fmt=qpd.RESID_INT4)
+    torch.cuda.synchronize()
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+    c_ref, s_ref = oracle.quantize_rows(h0.float().numpy())
+    np.testing.assert_array_equal(a[0].cpu().numpy(), c_ref)
+    np.testing.assert_array_equal(a[1].cpu().numpy(), s_ref)

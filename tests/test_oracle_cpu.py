@@ -311,9 +311,12 @@ def test_fast_vs_exact_mode(resid_fmt):
     """FAST (rne of t * RN(1/s), fma residual, scale*alpha folded) against
     EXACT (rne of the IEEE quotient, op-by-op rounding): two legal fp32
     evaluation orders of the same algorithm. Codes differ by at most one on
-    <= 0.01% of elements; scales agree to 1e-5 relative (bit-identical
-    scales are guaranteed only against an oracle with the same order, which
-    the GPU parity tests use)."""
+    <= 0.01% of elements. On these inputs (q, k not normalised, so h + k dv
+    cancels strongly) state scales differ by more than one ulp on about a
+    fifth of the rows, by at most 32 ulp (about 2e-6 relative); the
+    reference's own torch path differs from EXACT by more on the same
+    inputs (tests/test_torch_path_cpu.py). Bit-identical scales hold only
+    against an oracle with the same order, which the GPU parity tests use."""
     B, H, HV, K, V = 8, 32, 32, 128, 128
     pool = make_pool(B + 1, HV, V, K, resid_fmt, True, seed=6)
     mixed, a, b, A_log, dt = (x.numpy() for x in make_packed_inputs(B, H, HV, K, V, seed=9))
@@ -326,7 +329,9 @@ def test_fast_vs_exact_mode(resid_fmt):
     assert rel(of, oe) < 1e-5
     d = np.abs(pf[0].astype(np.int32) - pe[0].astype(np.int32))
     assert d.max() <= 1 and d.mean() <= 1e-4
-    assert np.max(np.abs(pf[1][1:] - pe[1][1:]) / pe[1][1:]) < 1e-5
+    su = np.abs(pf[1][1:].view(np.int32).astype(np.int64) - pe[1][1:].view(np.int32).astype(np.int64))
+    print(f"state scales: {np.mean(su > 1):.3f} of rows > 1 ulp apart, max {su.max()} ulp")
+    assert su.max() <= 32 and np.mean(su > 1) <= 0.25
     # residual codes: off by one, except where the state code flipped at a tie
     # (then the residual absorbs that state LSB; both pairs reconstruct the
     # same target)
@@ -487,3 +492,31 @@ def test_memory_claim():
     assert 1.9 < fp32 / q8 < 2.05 and bf16 / q8 < 1.1
     assert 2.5 < fp32 / q4 < 2.75 and bf16 / q4 > 1.25
     assert math.isclose(bf16 / q4, 1.28, abs_tol=0.005)
+
+
+def test_bf16_round_matches_torch():
+    """The oracle's fp32 -> bf16 rounding (numpy oracle.bf16_round and the C
+    bf16_round_f behind the bf16-state arm), which sets the expected values of
+    every bf16-state and bf16-output test, against torch's own
+    .to(torch.bfloat16): random values over the whole exponent range, exact
+    ties with an odd and an even kept bit, values just below and above the
+    point where rounding overflows to inf, subnormals, +-0, +-inf and NaN."""
+    import torch
+    rng = np.random.default_rng(12)
+    rand = rng.integers(0, 2 ** 32, 200_000, dtype=np.uint64).astype(np.uint32)
+    hi = rng.integers(0, 2 ** 16, 4000, dtype=np.uint64).astype(np.uint32) << 16
+    ties = np.concatenate([hi | 0x8000, hi | 0x7FFF, hi | 0x8001])          # exact ties and their neighbours
+    edges = np.array([0x7F7F7FFF, 0x7F7F8000, 0x7F7FFFFF, 0x7F7F0000,      # FLT_MAX region: stays / overflows
+                      0xFF7F8000, 0x00000001, 0x00008000, 0x00018000,       # subnormals, ties among them
+                      0x807FFFFF, 0x00000000, 0x80000000, 0x7F800000,       # +-0, +-inf
+                      0xFF800000, 0x7FC00000, 0x7F800001, 0xFFC12345], np.uint32)
+    x = np.concatenate([rand, ties, edges]).view(np.float32)
+    want = torch.from_numpy(x.copy()).to(torch.bfloat16).float().numpy()
+    for got in (oracle.bf16_round(x), oracle.bf16_round_c(x)):
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(got), nan)
+        np.testing.assert_array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+    # the ties really are ties, and both rounding directions occur
+    t = (hi | 0x8000).view(np.float32)
+    r = oracle.bf16_round(t).view(np.uint32)
+    assert np.any(r == hi) and np.any(r == hi + 0x10000)
