@@ -120,7 +120,7 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const void* __restri
   if (lane == 0) scale[row] = s;
 }
 
-// [M, K, V] matrices with K in {16, 32, 64, 128}, V % 4 == 0, 16-byte aligned:
+// [M, K, V] matrices with K in {16, 32, 64, 128, 256}, V % 4 == 0, 16-byte aligned:
 // a lane owns 4 consecutive columns over K/8 rows (its whole slice stays in
 // registers, no second read), lane = column group * 8 + K-slice, so one load
 // instruction reads 8 rows of 128 contiguous bytes; the column amax combines
@@ -229,13 +229,14 @@ extern "C" int ck_quantize_cols(const float* x, int64_t M, int K, int V, float q
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool aligned = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(codes) |
                          reinterpret_cast<uintptr_t>(scale)) & 15) == 0;
-  if (aligned && V % 4 == 0 && M <= 65535 && (K == 16 || K == 32 || K == 64 || K == 128)) {
+  if (aligned && V % 4 == 0 && M <= 65535 && (K == 16 || K == 32 || K == 64 || K == 128 || K == 256)) {
     const dim3 grid((unsigned)((V + 127) / 128), (unsigned)M);
     switch (K) {
       case 16: hipLaunchKernelGGL(quantize_cols4_kernel<16>, grid, dim3(256), 0, s, x, V, qmax, codes, scale); break;
       case 32: hipLaunchKernelGGL(quantize_cols4_kernel<32>, grid, dim3(256), 0, s, x, V, qmax, codes, scale); break;
       case 64: hipLaunchKernelGGL(quantize_cols4_kernel<64>, grid, dim3(256), 0, s, x, V, qmax, codes, scale); break;
-      default: hipLaunchKernelGGL(quantize_cols4_kernel<128>, grid, dim3(256), 0, s, x, V, qmax, codes, scale); break;
+      case 128: hipLaunchKernelGGL(quantize_cols4_kernel<128>, grid, dim3(256), 0, s, x, V, qmax, codes, scale); break;
+      default: hipLaunchKernelGGL(quantize_cols4_kernel<256>, grid, dim3(256), 0, s, x, V, qmax, codes, scale); break;
     }
     return check_launch("ck_quantize_cols");
   }

@@ -205,7 +205,10 @@ int ck_gdn_packed_decode_float_state(const void* mixed_qkv, int qkv_dtype, int64
  * residual, as the reference's GPU kernels do (cuda/gdn_state_kernel.cu:210,233).
  * e_scale_in / e_scale_out are read / written only for CK_RES_INT8.
  * In-place use (h_out == h_in, e_out == e_in, ...) is allowed.
- * Requirements: K in {16, 32, 64, 128}.
+ * Requirements: K in {16, 32, 64, 128, 256}; any V >= 1; fp32 tensors 4-byte
+ * and the residual element-size aligned. V % 4 == 0 with 16-byte aligned
+ * tensors takes one vector access per 4 columns, anything else one access
+ * per column (statequant/kernel.py:277-279 masks offs_v < V the same way).
  */
 int ck_gdn_quant_step(const int8_t* h_in, const float* scale_in, const void* e_in,
                       const float* e_scale_in,
@@ -215,7 +218,8 @@ int ck_gdn_quant_step(const int8_t* h_in, const float* scale_in, const void* e_i
                       int B, int HV, int K, int V, float qmax, int res_fmt, int quant_mode,
                       void* stream);
 
-/* FP32 baseline step in the statequant layout (no quantization). */
+/* FP32 baseline step in the statequant layout (no quantization); the same K,
+ * V and alignment rules as ck_gdn_quant_step. */
 int ck_gdn_fp32_step(const float* h_in, const float* q, const float* k, const float* v,
                      const float* alpha, const float* beta, float* o, float* h_out,
                      int B, int HV, int K, int V, void* stream);

@@ -135,7 +135,7 @@ void orc_gates_n(const float* a, const float* b, const float* A_log, const float
 /* Reductions in the fixed order described at the top.                       */
 /* ------------------------------------------------------------------------- */
 static float tree_sum(float* c, int n) {
-  /* balanced pairwise tree over n = 1, 2, 4, 8, 16 chunk sums (in place) */
+  /* balanced pairwise tree over n (a power of two, at most 64) sums, in place */
   for (int w = 1; w < n; w *= 2)
     for (int i = 0; i + w < n; i += 2 * w) c[i] = c[i] + c[i + w];
   return c[0];
@@ -452,25 +452,37 @@ void orc_e5m2_to_f32_n(const uint8_t* x, float* y, int64_t n) {
 
 /* ------------------------------------------------------------------------- */
 /* statequant layout: state [B, HV, K, V] (V contiguous), one scale per       */
-/* V-column (amax over K). K-reductions: the K rows split into 8 slices of    */
-/* K/8 consecutive rows; each slice is x0*y0 then fmaf over its rows; the 8   */
-/* slice sums combine as ((s0+s1)+(s2+s3))+((s4+s5)+(s6+s7)).                 */
+/* V-column (amax over K). K-reductions: the K rows split into S slices of    */
+/* consecutive rows, S = 8 for K <= 128 and K/16 (16 rows each) above; each   */
+/* slice is x0*y0 then fmaf over its rows; the S slice sums combine by a      */
+/* balanced pairwise tree (S = 8: ((s0+s1)+(s2+s3))+((s4+s5)+(s6+s7))).       */
 /* ------------------------------------------------------------------------- */
 #define RES_FP32 0
 #define RES_FP16 1
 #define RES_FP8 2
 #define RES_INT8 3
 
-static float dot_k8(const float* x, int64_t sx, const float* y, int K) {
-  float part[8];
-  const int rps = K / 8;
-  for (int sl = 0; sl < 8; ++sl) {
+static int statequant_slices(int K) { return K <= 128 ? 8 : K / 16; }
+
+static float dot_slices(const float* x, int64_t sx, const float* y, int K) {
+  float part[64];
+  const int ns = statequant_slices(K);
+  const int rps = K / ns;
+  for (int sl = 0; sl < ns; ++sl) {
     const int r0 = sl * rps;
     float acc = x[(int64_t)r0 * sx] * y[r0];
     for (int r = r0 + 1; r < r0 + rps; ++r) acc = fmaf(x[(int64_t)r * sx], y[r], acc);
     part[sl] = acc;
   }
-  return tree_sum(part, 8);
+  return tree_sum(part, ns);
+}
+
+/* K = 16, 32, 64, 128 (8 slices) or a multiple of 16 up to 1024 whose K/16 is a power of two */
+static int statequant_k_ok(int K) {
+  if (K < 16 || K > 1024 || K % 8 != 0) return 0;
+  if (K <= 128) return 1;
+  const int ns = K / 16;
+  return K % 16 == 0 && (ns & (ns - 1)) == 0;
 }
 
 /* statequant/kernel.py:149-178 (torch reference) and :260-341 (GPU kernel):
@@ -480,7 +492,7 @@ int orc_quant_step_kv(const int8_t* h_in, const float* scale_in, const void* e_i
                       const float* q, const float* k, const float* v, const float* alpha, const float* beta,
                       float* o, int8_t* h_out, float* scale_out, void* e_out, float* e_scale_out,
                       int B, int HV, int K, int V, float qmax, int res_fmt, int mode, int nthreads) {
-  if (K % 8 != 0 || K < 16) return 1;
+  if (!statequant_k_ok(K) || V <= 0) return 1;
   (void)nthreads;
 #ifdef _OPENMP
   if (nthreads > 0) omp_set_num_threads(nthreads);
@@ -503,10 +515,10 @@ int orc_quant_step_kv(const int8_t* h_in, const float* scale_in, const void* e_i
           h[(int64_t)r * V + c] = mode == MODE_FAST ? code * (scale_in[vb + c] * a) : (code * scale_in[vb + c]) * a;
         }
       /* delta rule (kernel.py:167-170) */
-      for (int c = 0; c < V; ++c) rd[c] = bt * (v[vb + c] - dot_k8(h + c, V, k + kb, K));
+      for (int c = 0; c < V; ++c) rd[c] = bt * (v[vb + c] - dot_slices(h + c, V, k + kb, K));
       for (int r = 0; r < K; ++r)
         for (int c = 0; c < V; ++c) h[(int64_t)r * V + c] = madd(k[kb + r], rd[c], h[(int64_t)r * V + c], mode);
-      for (int c = 0; c < V; ++c) o[vb + c] = dot_k8(h + c, V, q + kb, K);
+      for (int c = 0; c < V; ++c) o[vb + c] = dot_slices(h + c, V, q + kb, K);
       /* residual add (kernel.py:172) */
       for (int r = 0; r < K; ++r)
         for (int c = 0; c < V; ++c) {
@@ -564,16 +576,16 @@ int orc_quant_step_kv(const int8_t* h_in, const float* scale_in, const void* e_i
 /* FP32 GDN step in the statequant layout (statequant/kernel.py:116-123). */
 int orc_fp32_step_kv(const float* h_in, const float* q, const float* k, const float* v, const float* alpha,
                      const float* beta, float* o, float* h_out, int B, int HV, int K, int V) {
-  if (K % 8 != 0 || K < 16) return 1;
+  if (!statequant_k_ok(K) || V <= 0) return 1;
   float* rd = (float*)malloc(sizeof(float) * V);
   for (int64_t w = 0; w < (int64_t)B * HV; ++w) {
     const int64_t mb = w * (int64_t)K * V, vb = w * V, kb = w * K;
     float* h = h_out + mb;
     for (int64_t i = 0; i < (int64_t)K * V; ++i) h[i] = h_in[mb + i] * alpha[w];
-    for (int c = 0; c < V; ++c) rd[c] = beta[w] * (v[vb + c] - dot_k8(h + c, V, k + kb, K));
+    for (int c = 0; c < V; ++c) rd[c] = beta[w] * (v[vb + c] - dot_slices(h + c, V, k + kb, K));
     for (int r = 0; r < K; ++r)
       for (int c = 0; c < V; ++c) h[(int64_t)r * V + c] = fmaf(k[kb + r], rd[c], h[(int64_t)r * V + c]);
-    for (int c = 0; c < V; ++c) o[vb + c] = dot_k8(h + c, V, q + kb, K);
+    for (int c = 0; c < V; ++c) o[vb + c] = dot_slices(h + c, V, q + kb, K);
   }
   free(rd);
   return 0;

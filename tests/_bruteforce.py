@@ -9,8 +9,9 @@ order) shows up as a disagreement:
   vllm_integration/quantized_packed_decode.py:129-239  (vLLM layout)
   statequant/kernel.py:149-178, :296-341               (statequant layout)
 The fp32 evaluation order of the K-sums is the one the kernels define:
-chunks of 16 (vLLM layout) or 8 slices (statequant layout), each a
-sequential fma chain, combined as a balanced pairwise tree.
+chunks of 16 (vLLM layout) or slices of consecutive rows (statequant layout:
+8 slices of K/8 rows up to K = 128, 16 rows each above), each a sequential
+fma chain, combined as a balanced pairwise tree.
 """
 
 from __future__ import annotations
@@ -162,6 +163,7 @@ def packed_decode(mixed, a, b, A_log, dt_bias, scale, sc, ss, rc, rs, idx, H, *,
 def quant_step_kv(h_int8, scale, e, e_scale, q, k, v, alpha, beta, *, bits, res_fmt, exact):
     """One statequant-layout step; residual storage as in oracle.quant_step_kv."""
     B, HV, K, V = h_int8.shape
+    rows = K // 8 if K <= 128 else 16          # rows per K-slice
     qmax = F(2 ** (bits - 1) - 1)
     o = np.zeros((B, HV, V), F)
     h_out = np.zeros_like(h_int8)
@@ -179,9 +181,9 @@ def quant_step_kv(h_int8, scale, e, e_scale, q, k, v, alpha, beta, *, bits, res_
                     h = [F(F(F(int(h_int8[bb, hv, r, c])) * sc) * al) for r in range(K)]
                 else:
                     h = [F(F(int(h_int8[bb, hv, r, c])) * F(sc * al)) for r in range(K)]
-                dv = F(be * F(F(v[bb, hv, c]) - chunk_dot(h, kk, K // 8)))
+                dv = F(be * F(F(v[bb, hv, c]) - chunk_dot(h, kk, rows)))
                 h = [madd(kk[r], dv, h[r], exact) for r in range(K)]
-                o[bb, hv, c] = chunk_dot(h, qq, K // 8)
+                o[bb, hv, c] = chunk_dot(h, qq, rows)
                 if res_fmt == oracle.RES_INT8:
                     t = [madd(F(int(e[bb, hv, r, c])), F(e_scale[bb, hv, c]), h[r], exact) for r in range(K)]
                 elif res_fmt == oracle.RES_FP16:

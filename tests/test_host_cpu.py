@@ -82,8 +82,11 @@ def test_other_entry_points_argument_errors(L):
     p = ctypes.c_void_p(16)
     rc = L.ck_gdn_quant_step(p, p, p, p, p, p, p, p, p, p, p, p, p, p, 1, 1, 24, 8, 127.0, 0, 0, None)
     assert rc == _native.CK_EUNSUPPORTED and "K must be" in L.ck_last_error().decode()
-    rc = L.ck_gdn_quant_step(p, p, p, p, p, p, p, p, p, p, p, p, p, p, 1, 1, 32, 6, 127.0, 0, 0, None)
-    assert rc == _native.CK_EUNSUPPORTED and "multiple of 4" in L.ck_last_error().decode()
+    rc = L.ck_gdn_quant_step(p, p, p, p, p, p, p, p, p, p, p, p, p, p, 1, 1, 512, 6, 127.0, 0, 0, None)
+    assert rc == _native.CK_EUNSUPPORTED and "K must be" in L.ck_last_error().decode()
+    odd = ctypes.c_void_p(17)   # an fp16 residual at an odd address
+    rc = L.ck_gdn_quant_step(p, p, odd, p, p, p, p, p, p, p, p, p, p, p, 1, 1, 32, 6, 127.0, 1, 0, None)
+    assert rc == _native.CK_EINVAL and "2-byte aligned" in L.ck_last_error().decode()
     rc = L.ck_gdn_quant_step(p, p, p, p, p, p, p, p, p, p, p, p, p, p, 1, 1, 32, 8, 12.5, 0, 0, None)
     assert rc == _native.CK_EINVAL and "qmax" in L.ck_last_error().decode()
     rc = L.ck_gdn_quant_step(p, p, p, None, p, p, p, p, p, p, p, p, p, None, 1, 1, 32, 8, 127.0, 3, 0, None)

@@ -146,9 +146,12 @@ def test_packed_decode_matches_bruteforce(resid_fmt, per_head, exact, l2norm, bi
 
 @pytest.mark.parametrize("res_fmt", [oracle.RES_FP32, oracle.RES_FP16, oracle.RES_FP8, oracle.RES_INT8])
 @pytest.mark.parametrize("exact", [False, True])
-def test_quant_step_kv_matches_bruteforce(res_fmt, exact):
-    B, HV, K, V = 1, 2, 16, 4
-    rng = np.random.default_rng(res_fmt)
+@pytest.mark.parametrize("HV,K,V", [(2, 16, 4), (1, 64, 5), (1, 256, 3)])
+def test_quant_step_kv_matches_bruteforce(res_fmt, exact, HV, K, V):
+    """Every residual format and mode; K = 256 takes 16 slices of 16 rows,
+    smaller K 8 slices of K/8; V not a multiple of 4."""
+    B = 1
+    rng = np.random.default_rng(res_fmt + K)
     h0 = (rng.standard_normal((B, HV, K, V)) * 0.1).astype(F)
     codes, scale = oracle.quantize_cols(h0)
     res = (rng.standard_normal((B, HV, K, V)) * 1e-3).astype(F)
@@ -175,6 +178,47 @@ def test_quant_step_kv_matches_bruteforce(res_fmt, exact):
             assert g is None
         else:
             np.testing.assert_array_equal(g, r)
+
+
+def _slice_order_case(K, V, rows):
+    """Inputs whose h^T q is exact per product: beta = 0 (h is its dequantized
+    codes), alpha = scale = 1, code 1 in each listed row with q carrying the
+    value; every other code and q is 0."""
+    codes = np.zeros((1, 1, K, V), np.int8)
+    q = np.zeros((1, 1, K), F)
+    for r, val in rows:
+        codes[0, 0, r, :] = 1
+        q[0, 0, r] = val
+    z = np.zeros
+    return (codes, np.ones((1, 1, V), F), z((1, 1, K, V), F), None, q, z((1, 1, K), F), z((1, 1, V), F),
+            np.ones((1, 1), F), z((1, 1), F))
+
+
+def statequant_slices(K):
+    return 8 if K <= 128 else K // 16
+
+
+@pytest.mark.parametrize("K", [16, 32, 64, 128, 256])
+@pytest.mark.parametrize("mode", [oracle.MODE_FAST, oracle.MODE_EXACT])
+def test_statequant_reduction_order_known_answer(K, mode):
+    """Closed forms that fix the K-sum order of the statequant step.
+    (a) 2^24 at row 0 and 1 at rows R and R+1 (R = rows per slice): the slice
+    holding rows R, R+1 sums them to 2 before meeting 2^24, giving 2^24 + 2;
+    slices twice as long, or one sequential chain, would add each 1 to 2^24
+    separately and round back to 2^24. (b) 2^24 at row 0 and 1 at the first
+    row of every other slice: a balanced tree over S slices loses only the 1
+    paired with 2^24 at its first level, giving 2^24 + S - 2; a sequential
+    pass over the slices would give 2^24."""
+    S = statequant_slices(K)
+    R = K // S
+    big = F(2.0 ** 24)
+    for rows, want in (([(0, big), (R, 1.0), (R + 1, 1.0)], big + 2),
+                       ([(0, big)] + [(s * R, 1.0) for s in range(1, S)], big + S - 2)):
+        o = oracle.quant_step_kv(*_slice_order_case(K, 3, rows), mode=mode)[0]
+        assert np.all(o == want), (K, rows[:3], o.ravel(), want)
+        ref = bf.quant_step_kv(*_slice_order_case(K, 1, rows), bits=8, res_fmt=oracle.RES_FP32,
+                               exact=mode == oracle.MODE_EXACT)[0]
+        assert np.all(ref == want)
 
 
 # ---------------------------------------------------------------------------
@@ -446,11 +490,12 @@ def test_quantize_rows_cols_match_torch_round():
     np.testing.assert_array_equal(c2, torch.round(x / s_t2[..., None, :]).clamp(-127, 127).to(torch.int8).numpy())
 
 
-def test_fp32_step_vs_float64():
+@pytest.mark.parametrize("K,V", [(64, 32), (256, 130)])
+def test_fp32_step_vs_float64(K, V):
     rng = np.random.default_rng(3)
-    h = (rng.standard_normal((2, 4, 64, 32)) * 0.1).astype(F)
-    q, k = (rng.standard_normal((2, 4, 64)).astype(F) for _ in range(2))
-    v = rng.standard_normal((2, 4, 32)).astype(F)
+    h = (rng.standard_normal((2, 4, K, V)) * 0.1).astype(F)
+    q, k = (rng.standard_normal((2, 4, K)).astype(F) for _ in range(2))
+    v = rng.standard_normal((2, 4, V)).astype(F)
     al, be = F(rng.uniform(0.9, 1, (2, 4))), F(rng.uniform(0, 1, (2, 4)))
     h1, o1 = oracle.fp32_step_kv(h, q, k, v, al, be)
     h2, o2 = oracle.gdn_step_f64(h, q, k, v, al, be)

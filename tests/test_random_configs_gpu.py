@@ -101,8 +101,9 @@ def test_random_statequant_step_bit_exact(device, seed):
     from tests.test_statequant_gpu import _random_state, _storage, make_inputs
 
     rng = np.random.default_rng(5000 + seed)
-    K = int(rng.choice([16, 32, 64, 128]))
-    V = 4 * int(rng.integers(1, 50))                  # the layout's lanes take 4 columns each
+    K = int(rng.choice([16, 32, 64, 128, 256]))
+    # half the draws a multiple of 4 (vector column groups), half any V
+    V = 4 * int(rng.integers(1, 50)) if rng.random() < 0.5 else int(rng.integers(1, 200))
     B, HV = int(rng.integers(1, 4)), int(rng.integers(1, 9))
     res_fmt = int(rng.integers(4))
     mode = "exact" if rng.random() < 0.4 else "fast"

@@ -58,8 +58,12 @@ def _random_state(B, HV, K, V, res_fmt, seed, bits=8):
 
 @pytest.mark.parametrize("res_fmt", [sq.RES_FP32, sq.RES_FP16, sq.RES_FP8, sq.RES_INT8])
 @pytest.mark.parametrize("mode", ["fast", "exact"])
-@pytest.mark.parametrize("K,V,B,HV", [(128, 128, 2, 32), (64, 64, 1, 4), (32, 8, 1, 1), (16, 136, 2, 3)])
+@pytest.mark.parametrize("K,V,B,HV", [(128, 128, 2, 32), (64, 64, 1, 4), (32, 8, 1, 1), (16, 136, 2, 3),
+                                     (256, 128, 1, 4), (128, 130, 1, 3), (256, 130, 2, 2), (16, 3, 2, 2),
+                                     (64, 67, 1, 2)])
 def test_step_bit_exact_vs_oracle(device, res_fmt, mode, K, V, B, HV):
+    """K = 256 runs 16 slices of 16 rows; V not a multiple of 4 (130, 3, 67)
+    takes the per-column access path with a partial last column group."""
     h_int8, scale, e, es = _random_state(B, HV, K, V, res_fmt, seed=K + V + res_fmt)
     _, q, k, v, alpha, beta = make_inputs(1, B, HV, K, V, seed=5)
     beta = beta[0] * 0 + torch.rand(B, HV, generator=torch.Generator().manual_seed(9))
@@ -95,7 +99,7 @@ def test_int6_state_int8_residual(device):
     assert int(got[1].abs().max()) <= 31 and int(got[3].abs().max()) <= 31
 
 
-@pytest.mark.parametrize("K,V", [(128, 128), (32, 8)])
+@pytest.mark.parametrize("K,V", [(128, 128), (32, 8), (256, 128), (256, 130), (64, 3)])
 def test_fp32_step_bit_exact(device, K, V):
     h0, q, k, v, alpha, beta = make_inputs(1, 2, 4, K, V, seed=7)
     h_g, o_g = binding.gdn_fp32_step_hip(h0.to(device), q[0].to(device), k[0].to(device), v[0].to(device),
@@ -108,6 +112,64 @@ def test_fp32_step_bit_exact(device, K, V):
     h64, o64 = oracle.gdn_step_f64(h0.numpy(), q[0].numpy(), k[0].numpy(), v[0].numpy(), alpha[0].numpy(),
                                    beta[0].numpy())
     assert np.abs(h_g.cpu().numpy() - h64).max() < 1e-3 and np.abs(o_g.cpu().numpy() - o64).max() < 1e-3
+
+
+def _shifted(t: torch.Tensor) -> torch.Tensor:
+    """A contiguous copy of t that starts one element into its allocation, so
+    its address is not 16-byte aligned."""
+    buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=t.device)
+    out = buf[1:].view(t.shape)
+    out.copy_(t)
+    return out
+
+
+@pytest.mark.parametrize("res_fmt", [sq.RES_FP32, sq.RES_FP16, sq.RES_FP8, sq.RES_INT8])
+def test_step_unaligned_tensors(device, res_fmt):
+    """V = 128 but every input starts one element past an aligned address:
+    the host picks the per-column access path, which must match the oracle."""
+    B, HV, K, V = 2, 3, 64, 128
+    h_int8, scale, e, es = _random_state(B, HV, K, V, res_fmt, seed=40 + res_fmt)
+    _, q, k, v, alpha, beta = make_inputs(1, B, HV, K, V, seed=11)
+    args = [h_int8, scale, e, es, q[0], k[0], v[0], alpha[0], beta[0]]
+    dev_args = [None if a is None else _shifted(a.to(device)) for a in args]
+    assert all(a is None or a.data_ptr() % 16 for a in dev_args)
+    print(f"case unaligned res={res_fmt}", flush=True)
+    got = sq.gdn_quant_step_fused(*dev_args, bits=8, res_fmt=res_fmt)
+    torch.cuda.synchronize()
+    ref = oracle.quant_step_kv(h_int8.numpy(), scale.numpy(), _storage(e, res_fmt),
+                               None if es is None else es.numpy(), q[0].numpy(), k[0].numpy(), v[0].numpy(),
+                               alpha[0].numpy(), beta[0].numpy(), bits=8, res_fmt=res_fmt)
+    for name, g_, r_ in zip(("o", "h_int8", "scale", "e", "e_scale"), got, ref):
+        if r_ is not None:
+            g_np = _storage(g_, res_fmt) if name == "e" else g_.cpu().numpy()
+            np.testing.assert_array_equal(g_np, r_, err_msg=f"{name} differs")
+
+
+@pytest.mark.parametrize("K", [16, 64, 128, 256])
+@pytest.mark.parametrize("V", [4, 5])
+def test_reduction_order_known_answer(device, K, V):
+    """The closed forms that fix the K-sum order (the oracle's CPU test holds
+    the derivation): beta = 0 and alpha = scale = 1 make o = sum over rows of
+    code * q exactly per product. 2^24 at row 0 with 1 at rows R, R+1 of the
+    next slice gives 2^24 + 2; 2^24 at row 0 with 1 at the first row of every
+    other slice gives 2^24 + S - 2 (S slices of R rows: 8 up to K = 128, K/16
+    at K = 256)."""
+    S = 8 if K <= 128 else K // 16
+    R = K // S
+    big = 2.0 ** 24
+    z = dict(device=device)
+    for rows, want in (([(0, big), (R, 1.0), (R + 1, 1.0)], big + 2),
+                       ([(0, big)] + [(s * R, 1.0) for s in range(1, S)], big + S - 2)):
+        codes = torch.zeros(1, 1, K, V, dtype=torch.int8, **z)
+        q = torch.zeros(1, 1, K, **z)
+        for r, val in rows:
+            codes[0, 0, r, :] = 1
+            q[0, 0, r] = val
+        for mode in ("fast", "exact"):
+            o = sq.gdn_quant_step_fused(codes, torch.ones(1, 1, V, **z), torch.zeros(1, 1, K, V, **z), None, q,
+                                        torch.zeros(1, 1, K, **z), torch.zeros(1, 1, V, **z),
+                                        torch.ones(1, 1, **z), torch.zeros(1, 1, **z), quant_mode=mode)[0]
+            assert torch.all(o.cpu() == want), (K, V, mode, o.cpu().ravel().tolist(), want)
 
 
 def test_per_v_channel_quantize(device):
@@ -195,7 +257,7 @@ def test_batch8_step(device):
         np.testing.assert_array_equal(g_.cpu().numpy(), r_)
 
 
-@pytest.mark.parametrize("K", [16, 32, 64, 128])
+@pytest.mark.parametrize("K", [16, 32, 64, 128, 256])
 @pytest.mark.parametrize("V", [4, 36, 200, 7])
 def test_per_v_channel_quantize_shapes_and_ties(device, K, V):
     """Every K of the vectorised column kernel, V below and above one
