@@ -5,10 +5,19 @@
 
 #include <mutex>
 
-#include "packed_decode_impl.h"
+#include "packed_decode_masked.h"
 
 namespace ck {
 namespace pd {
+
+int launch_masked(const PackedParams& p, int B, int resid_fmt, int per_head, int mode, bool lanes,
+                  hipStream_t stream) {
+  if (p.K <= 16) return launch_masked_k<16>(p, B, resid_fmt, per_head, mode, lanes, stream);
+  if (p.K <= 32) return launch_masked_k<32>(p, B, resid_fmt, per_head, mode, lanes, stream);
+  if (p.K <= 64) return launch_masked_k<64>(p, B, resid_fmt, per_head, mode, lanes, stream);
+  if (p.K <= 128) return launch_masked_k<128>(p, B, resid_fmt, per_head, mode, lanes, stream);
+  return launch_masked_k<256>(p, B, resid_fmt, per_head, mode, lanes, stream);
+}
 
 int resident_workgroups(const void* fn, int block, int* per_cu_out) {
   static std::mutex mu;
@@ -81,18 +90,21 @@ static int packed_decode_impl(const void* mixed_qkv, int qkv_dtype, int64_t stri
     return fail(CK_EINVAL, "quant_mode must be CK_QUANT_FAST or CK_QUANT_EXACT, got %d", quant_mode);
   if (state_bits < 2 || state_bits > 8) return fail(CK_EINVAL, "state_bits must be in 2..8, got %d", state_bits);
   if (num_slots <= 0) return fail(CK_EINVAL, "num_slots must be positive");
-  if (K != 16 && K != 32 && K != 64 && K != 128 && K != 256)
-    return fail(CK_EUNSUPPORTED, "K must be one of 16, 32, 64, 128, 256, got %d", K);
+  if (K > 256) return fail(CK_EUNSUPPORTED, "K must be at most 256, got %d", K);
+  if (resid_fmt == CK_RESID_INT4 && K % 2 != 0)
+    return fail(CK_EINVAL, "int4 residual packing needs an even K, got %d", K);
   if (B == 0) return ok();
   if (!mixed_qkv || !a || !b || !A_log || !dt_bias || !state_codes || !state_scale || !resid_codes || !resid_scale ||
       !out || !ssm_state_indices)
     return fail(CK_EINVAL, "null pointer argument");
-  // lanes load 16 state bytes and 8 (int4) or 16 (int8) residual bytes
+  // The bandwidth kernels take power-of-two K from 16 and rows their lanes
+  // load whole (16 state bytes and 8 (int4) or 16 (int8) residual bytes per
+  // lane); any other K or row alignment runs the masked kernel.
   const int ealign = (resid_fmt == CK_RESID_INT4) ? 8 : 16;
-  if ((reinterpret_cast<uintptr_t>(state_codes) & 15) || (stride_state_slot % 16))
-    return fail(CK_EINVAL, "state_codes rows must be 16-byte aligned");
-  if ((reinterpret_cast<uintptr_t>(resid_codes) & (ealign - 1)) || (stride_resid_slot % ealign))
-    return fail(CK_EINVAL, "resid_codes rows must be %d-byte aligned", ealign);
+  const bool pow2_k = K == 16 || K == 32 || K == 64 || K == 128 || K == 256;
+  const bool rows_aligned = !(reinterpret_cast<uintptr_t>(state_codes) & 15) && stride_state_slot % 16 == 0 &&
+                            !(reinterpret_cast<uintptr_t>(resid_codes) & (ealign - 1)) &&
+                            stride_resid_slot % ealign == 0;
   // per-lane offsets inside one (slot, head) and one row of mixed_qkv are 32-bit
   if ((int64_t)V * K >= ((int64_t)1 << 31) || (2 * (int64_t)H * K + (int64_t)HV * V) * 4 >= ((int64_t)1 << 31))
     return fail(CK_EUNSUPPORTED, "head or activation row too large");
@@ -136,6 +148,7 @@ static int packed_decode_impl(const void* mixed_qkv, int qkv_dtype, int64_t stri
   p.H = H;
   p.HV = HV;
   p.V = V;
+  p.K = K;
   p.l2norm = use_qk_l2norm ? 1 : 0;
 #if CK_TIMELINE
   p.timeline = static_cast<uint64_t*>(g_timeline);
@@ -143,6 +156,7 @@ static int packed_decode_impl(const void* mixed_qkv, int qkv_dtype, int64_t stri
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int per_head = rscale_mode == CK_RSCALE_PER_HEAD;
   const int mode = quant_mode == CK_QUANT_EXACT ? kExact : kFast;
+  if (!pow2_k || !rows_aligned) return launch_masked(p, B, resid_fmt, per_head, mode, rows_aligned && K % 16 == 0, s);
   switch (K) {
     case 16: return launch_for_k<16>(p, B, resid_fmt, per_head, mode, qkv_dtype, s);
     case 32: return launch_for_k<32>(p, B, resid_fmt, per_head, mode, qkv_dtype, s);

@@ -89,6 +89,7 @@ struct PackedParams {
   float qmax, rqmax;      // state code range and RN(1/qmax)
   int32_t dtypes;         // mixed | a << 4 | b << 8 | A_log << 12 | dt_bias << 16 | out << 20
   int32_t H, HV, V;
+  int32_t K;              // pool row length; the template K of the masked kernel is K rounded up to a power of two
   int32_t items;          // B * HV * nvt
   int32_t l2norm;
   int32_t cu_share_n;     // workgroups per CU that share their items unevenly (<= 1: plain stride); see work_seq
@@ -309,8 +310,41 @@ __device__ __forceinline__ void stage_qk(const PackedParams& p, const uint32_t (
   __syncthreads();
 }
 
-// Compute and store one item whose registers are loaded.
-template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ACT, bool DST>
+// The first n bytes (n clamped to 0 .. 4 NW) of w, byte j from dword j / 4,
+// one byte store each: the masked kernel's rows have any length and alignment.
+template <int NW>
+__device__ __forceinline__ void st_bytes_masked(int8_t* dst, const uint32_t (&w)[NW], int n) {
+#pragma unroll
+  for (int j = 0; j < 4 * NW; ++j)
+    if (j < n) dst[j] = (int8_t)(w[j >> 2] >> (8 * (j & 3)));
+}
+
+template <int RESID>
+__device__ __forceinline__ void store_resid_masked(int8_t* dst, const uint32_t (&eb)[16], int n) {
+  if constexpr (RESID == kResidInt4) {
+    const uint32_t w0[8] = {eb[0], eb[1], eb[2], eb[3], eb[4], eb[5], eb[6], eb[7]};
+    const uint32_t w1[8] = {eb[8], eb[9], eb[10], eb[11], eb[12], eb[13], eb[14], eb[15]};
+    const uint32_t w[2] = {pack_nibbles8(w0), pack_nibbles8(w1)};
+    st_bytes_masked<2>(dst, w, n);
+  } else {
+    const uint32_t w[4] = {pack_low_bytes(eb[0], eb[1], eb[2], eb[3]), pack_low_bytes(eb[4], eb[5], eb[6], eb[7]),
+                           pack_low_bytes(eb[8], eb[9], eb[10], eb[11]), pack_low_bytes(eb[12], eb[13], eb[14], eb[15])};
+    st_bytes_masked<4>(dst, w, n);
+  }
+}
+
+// How the masked kernel's rows are accessed: rows are p.K codes long (K is
+// p.K rounded up to a power of two, at least 16; the loader zero-fills every
+// value past p.K). kMaskBytes: any p.K and alignment, byte by byte.
+// kMaskLanes: p.K a multiple of 16 with aligned rows, so a lane's 16 codes
+// (and 8 or 16 residual bytes) are all there or all past p.K, and it loads and
+// stores them whole.
+constexpr int kMaskNone = 0;
+constexpr int kMaskBytes = 1;
+constexpr int kMaskLanes = 2;
+
+// Compute and store one item whose registers are loaded (MASK: see above).
+template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ACT, bool DST, int MASK = kMaskNone>
 __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCoord& ic, int row0, int c, int lane,
                                              int wave, int parity, float alpha, float beta,
                                              const ItemRegs<RPL, Layout<K, RPL, WAVES, RESID, PER_HEAD>::EW,
@@ -347,8 +381,13 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
   // step is in place); a destination outside [1, num_slots) stores nothing
   const bool dst_ok = DST ? ic.dlive : true;
   const int64_t dslot = DST ? (ic.dlive ? ic.dslot : 0) : ic.slot;
-  int8_t* sbase = p.state + dslot * p.stride_state + (int64_t)ic.hv * p.V * K;
-  int8_t* ebase = p.resid + dslot * p.stride_resid + (int64_t)ic.hv * p.V * L::RK;
+  constexpr bool MASKED = MASK != kMaskNone;
+  const int KA = MASKED ? p.K : K;  // state bytes per row
+  const int RKA = MASKED ? (RESID == kResidInt4 ? p.K / 2 : p.K) : L::RK;  // residual bytes per row
+  const bool lane_in = MASK != kMaskLanes || c * 16 < KA;  // kMaskLanes: the lane's bytes exist
+  constexpr int RKL = L::RK / LPR;  // residual bytes per lane
+  int8_t* sbase = p.state + dslot * p.stride_state + (int64_t)ic.hv * p.V * KA;
+  int8_t* ebase = p.resid + dslot * p.stride_resid + (int64_t)ic.hv * p.V * RKA;
   float* scb = p.sscale + dslot * p.stride_sscale + (int64_t)ic.hv * p.V;
   float* rsb = PER_HEAD ? p.rscale + dslot * p.stride_rscale + ic.hv
                         : p.rscale + dslot * p.stride_rscale + (int64_t)ic.hv * p.V;
@@ -433,9 +472,15 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
     }
     const bool store = valid && dst_ok;
     if (store) {
-      st_stream16(sbase + (uint32_t)(r * K + c * 16),
-                  u32x4{pack_low_bytes(yb[0], yb[1], yb[2], yb[3]), pack_low_bytes(yb[4], yb[5], yb[6], yb[7]),
-                        pack_low_bytes(yb[8], yb[9], yb[10], yb[11]), pack_low_bytes(yb[12], yb[13], yb[14], yb[15])});
+      const uint32_t w[4] = {pack_low_bytes(yb[0], yb[1], yb[2], yb[3]), pack_low_bytes(yb[4], yb[5], yb[6], yb[7]),
+                             pack_low_bytes(yb[8], yb[9], yb[10], yb[11]), pack_low_bytes(yb[12], yb[13], yb[14], yb[15])};
+      if constexpr (MASK == kMaskBytes) {
+        st_bytes_masked<4>(sbase + (uint32_t)(r * KA + c * 16), w, KA - c * 16);
+      } else if constexpr (MASK == kMaskLanes) {
+        if (lane_in) st_stream16(sbase + (uint32_t)(r * KA + c * 16), u32x4{w[0], w[1], w[2], w[3]});
+      } else {
+        st_stream16(sbase + (uint32_t)(r * K + c * 16), u32x4{w[0], w[1], w[2], w[3]});
+      }
       if (c == 0) st_at<float>(scb, (uint32_t)r * 4u, s_new);
     }
 
@@ -461,7 +506,11 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
 #pragma unroll
       for (int j = 0; j < 16; ++j) (void)quantize<MODE>(t[j], es, inv_e, eb[j]);
       if (store) {
-        store_resid<RESID>(ebase + (uint32_t)(r * L::RK + c * (L::RK / LPR)), eb);
+        if constexpr (MASK == kMaskBytes) {
+          store_resid_masked<RESID>(ebase + (uint32_t)(r * RKA + c * RKL), eb, RKA - c * RKL);
+        } else if (lane_in) {
+          store_resid<RESID>(ebase + (uint32_t)(r * RKA + c * RKL), eb);
+        }
         if (c == 0) st_at<float>(rsb, (uint32_t)r * 4u, es);
       }
     }
@@ -492,7 +541,13 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
         }
         (void)quantize<MODE>(ev, es, inv_e, eb[j]);
       }
-      if (r < p.V && dst_ok) store_resid<RESID>(ebase + (uint32_t)(r * L::RK + c * (L::RK / LPR)), eb);
+      if (r < p.V && dst_ok) {
+        if constexpr (MASK == kMaskBytes) {
+          store_resid_masked<RESID>(ebase + (uint32_t)(r * RKA + c * RKL), eb, RKA - c * RKL);
+        } else if (lane_in) {
+          store_resid<RESID>(ebase + (uint32_t)(r * RKA + c * RKL), eb);
+        }
+      }
     }
     if (threadIdx.x == 0 && dst_ok) *rsb = es;
   }
@@ -812,6 +867,13 @@ int launch_for_act(const PackedParams& p, int B, int resid_fmt, int per_head, in
 
 template <int K>
 int launch_for_k(const PackedParams& p, int B, int resid_fmt, int per_head, int mode, int act, hipStream_t stream);
+
+// Any K in 1 .. 256 and any row alignment (packed_decode_masked.h): the lane
+// map of K rounded up to a power of two (at least 16), values past p.K zero,
+// one item per workgroup; lanes: whole-lane accesses (p.K a multiple of 16,
+// aligned rows), else byte-granular ones.
+int launch_masked(const PackedParams& p, int B, int resid_fmt, int per_head, int mode, bool lanes,
+                  hipStream_t stream);
 
 #define CK_PD_DEFINE_LAUNCH_FOR_K(KV)                                                                     \
   template <>                                                                                             \

@@ -55,7 +55,10 @@ RESID_INT4 = 1
 
 HAS_HIP = _native.library_available()
 
-SUPPORTED_K = (16, 32, 64, 128, 256)
+# The reference takes any K (its BK = next_pow2(K) lanes are masked past K);
+# here K up to 256. Power-of-two K from 16 with 16-byte aligned pool rows run
+# the bandwidth kernel, every other K or row alignment the masked kernel.
+MAX_K = 256
 
 _QUANT_MODES = {"fast": _native.QUANT_FAST, "exact": _native.QUANT_EXACT}
 
@@ -178,8 +181,8 @@ def quantized_gated_delta_rule_packed_decode(
         raise ValueError(f"cannot infer H from mixed_qkv width {qkv_dim}")
     if resid_fmt == RESID_INT4 and K % 2 != 0:
         raise ValueError(f"int4 residual packing needs an even K, got {K}")
-    if K not in SUPPORTED_K:
-        raise ValueError(f"packed decode supports K in {SUPPORTED_K}, got K={K}")
+    if K > MAX_K:
+        raise ValueError(f"packed decode supports K <= {MAX_K}, got K={K}")
 
     # checks the reference leaves implicit
     ss_sh, rs_sh = state_scale.shape, resid_scale.shape

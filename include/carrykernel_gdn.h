@@ -95,8 +95,14 @@ int ck_abi_version(void);
  *   block (out gets zeros, state untouched); slot >= num_slots is out of range
  *   (out gets NaN, state untouched).
  * state_bits: the state code range is +-(2^(state_bits-1) - 1), bits in 2..8.
- * Requirements: K in {16, 32, 64, 128, 256}; HV % H == 0; 16-byte aligned
- *   state rows (8-byte for int4 residual rows).
+ * Requirements: K in 1..256 (even for CK_RESID_INT4); HV % H == 0. Rows of
+ *   K = 16, 32, 64, 128 or 256 codes, 16-byte aligned (8-byte for int4
+ *   residual rows), run the bandwidth kernel; any other K or alignment runs
+ *   the masked kernel, which computes as if every row, q and k were
+ *   zero-padded to max(16, next_pow2(K)), as the reference's masked lanes do
+ *   (quantized_packed_decode.py:123-127,158,165-166,303), with whole 16-byte
+ *   lane accesses when K is a multiple of 16 and rows are aligned, byte
+ *   accesses otherwise.
  */
 int ck_gdn_packed_decode(const void* mixed_qkv, int qkv_dtype, int64_t stride_qkv_tok,
                          const void* a, int a_dtype, int64_t stride_a_tok,

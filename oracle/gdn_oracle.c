@@ -209,8 +209,15 @@ int orc_packed_decode(const float* mixed, int64_t stride_mixed,
                       int B, int H, int HV, int K, int V,
                       int l2norm, int resid_fmt, int per_head, int state_bits, int mode, int nthreads) {
   /* dst_idx (may be NULL: in place): the updated state of request n goes to
-     slot dst_idx[n]; one outside [1, num_slots) discards it (out is kept). */
-  if (K % 16 != 0 || K > 256 || (K / 16 & (K / 16 - 1)) != 0 || HV % H != 0) return 1;
+     slot dst_idx[n]; one outside [1, num_slots) discards it (out is kept).
+     Any K in 1..256 (even for the int4 residual): the reference's lanes
+     o_k < BK = next_pow2(K) load 0 past K (qpd:123-127, :158, :165-166,
+     :196-202, :303), so the step runs on rows zero-padded to
+     KP = max(16, next_pow2(K)) in the reduction order of KP and stores the
+     K existing columns. */
+  if (K < 1 || K > 256 || HV % H != 0 || (resid_fmt == 1 && K % 2 != 0)) return 1;
+  int KP = 16;
+  while (KP < K) KP *= 2;
   const float qmax = (float)((1 << (state_bits - 1)) - 1);
   const float qmax_e = resid_fmt == 1 ? 7.0f : 127.0f;
   const int RK = resid_fmt == 1 ? K / 2 : K;
@@ -221,11 +228,11 @@ int orc_packed_decode(const float* mixed, int64_t stride_mixed,
 #pragma omp parallel
 #endif
   {
-    float* q = (float*)malloc(sizeof(float) * K);
-    float* k = (float*)malloc(sizeof(float) * K);
-    float* h = (float*)malloc(sizeof(float) * K);
-    float* ebuf = (float*)malloc(sizeof(float) * (size_t)V * K);
-    int* codes = (int*)malloc(sizeof(int) * K);
+    float* q = (float*)malloc(sizeof(float) * KP);
+    float* k = (float*)malloc(sizeof(float) * KP);
+    float* h = (float*)malloc(sizeof(float) * KP);
+    float* ebuf = (float*)malloc(sizeof(float) * (size_t)V * KP);
+    int* codes = (int*)malloc(sizeof(int) * KP);
 #ifdef _OPENMP
 #pragma omp for schedule(static)
 #endif
@@ -241,19 +248,19 @@ int orc_packed_decode(const float* mixed, int64_t stride_mixed,
       }
       const int hq = hv / (HV / H);
       const float* m = mixed + (int64_t)n * stride_mixed;
-      for (int j = 0; j < K; ++j) {
-        q[j] = m[(int64_t)hq * K + j];
-        k[j] = m[(int64_t)H * K + (int64_t)hq * K + j];
+      for (int j = 0; j < KP; ++j) {
+        q[j] = j < K ? m[(int64_t)hq * K + j] : 0.0f;
+        k[j] = j < K ? m[(int64_t)H * K + (int64_t)hq * K + j] : 0.0f;
       }
       if (l2norm) { /* qpd:169-171 */
-        const float dq = sqrtf(dot_k(q, 1, q, 1, K) + 1e-6f);
-        const float dk = sqrtf(dot_k(k, 1, k, 1, K) + 1e-6f);
-        for (int j = 0; j < K; ++j) {
+        const float dq = sqrtf(dot_k(q, 1, q, 1, KP) + 1e-6f);
+        const float dk = sqrtf(dot_k(k, 1, k, 1, KP) + 1e-6f);
+        for (int j = 0; j < KP; ++j) {
           q[j] = q[j] / dq;
           k[j] = k[j] / dk;
         }
       }
-      for (int j = 0; j < K; ++j) q[j] = q[j] * scale; /* qpd:172 */
+      for (int j = 0; j < KP; ++j) q[j] = q[j] * scale; /* qpd:172 */
       float alpha, beta;
       orc_gates(a[(int64_t)n * stride_a + hv], b[(int64_t)n * stride_b + hv], A_log[hv], dt_bias[hv], &alpha, &beta);
 
@@ -280,38 +287,38 @@ int orc_packed_decode(const float* mixed, int64_t stride_mixed,
         /* dequantize + decay (qpd:158, :185) */
         if (mode == MODE_FAST) {
           const float sa = ss[r] * alpha;
-          for (int j = 0; j < K; ++j) h[j] = (float)crow[j] * sa;
+          for (int j = 0; j < KP; ++j) h[j] = (float)(j < K ? crow[j] : 0) * sa;
         } else {
-          for (int j = 0; j < K; ++j) h[j] = ((float)crow[j] * ss[r]) * alpha;
+          for (int j = 0; j < KP; ++j) h[j] = ((float)(j < K ? crow[j] : 0) * ss[r]) * alpha;
         }
         /* delta rule (qpd:186-190) */
-        const float rd = dot_k(h, 1, k, 1, K);
+        const float rd = dot_k(h, 1, k, 1, KP);
         const float dv = beta * (vv[r] - rd);
-        for (int j = 0; j < K; ++j) h[j] = madd(k[j], dv, h[j], mode);
-        o[r] = dot_k(h, 1, q, 1, K);
+        for (int j = 0; j < KP; ++j) h[j] = madd(k[j], dv, h[j], mode);
+        o[r] = dot_k(h, 1, q, 1, KP);
         /* residual add (qpd:195-203) */
         const float es_in = per_head ? rs_head : rs[r];
-        for (int j = 0; j < K; ++j) {
-          const int ec = resid_fmt == 1 ? unpack_i4(erow, j) : (int)erow[j];
+        for (int j = 0; j < KP; ++j) {
+          const int ec = j >= K ? 0 : resid_fmt == 1 ? unpack_i4(erow, j) : (int)erow[j];
           h[j] = madd((float)ec, es_in, h[j], mode);
         }
         /* requantize (qpd:205-209) */
         float am = 0.0f;
-        for (int j = 0; j < K; ++j) am = fmaxf(am, fabsf(h[j]));
+        for (int j = 0; j < KP; ++j) am = fmaxf(am, fabsf(h[j]));
         const float s_new = fmaxf(am / qmax, ORC_EPS);
         const float inv = 1.0f / s_new;
-        float* e = ebuf + (int64_t)r * K;
-        for (int j = 0; j < K; ++j) {
+        float* e = ebuf + (int64_t)r * KP;
+        for (int j = 0; j < KP; ++j) {
           const float c = quant_code(h[j], s_new, inv, qmax, mode);
-          if (store) crow_w[j] = (int8_t)c;
+          if (store && j < K) crow_w[j] = (int8_t)c;
           e[j] = resid_of(h[j], c, s_new, mode);
         }
         if (store) ss_w[r] = s_new;
         if (per_head) {
-          for (int j = 0; j < K; ++j) ea_head = fmaxf(ea_head, fabsf(e[j]));
+          for (int j = 0; j < KP; ++j) ea_head = fmaxf(ea_head, fabsf(e[j]));
         } else { /* residual quantize, per V-row scale (qpd:211-215) */
           float ea = 0.0f;
-          for (int j = 0; j < K; ++j) ea = fmaxf(ea, fabsf(e[j]));
+          for (int j = 0; j < KP; ++j) ea = fmaxf(ea, fabsf(e[j]));
           const float es = fmaxf(ea / qmax_e, ORC_EPS);
           const float inv_e = 1.0f / es;
           for (int j = 0; j < K; ++j) codes[j] = (int)quant_code(e[j], es, inv_e, qmax_e, mode);
@@ -329,7 +336,7 @@ int orc_packed_decode(const float* mixed, int64_t stride_mixed,
         const float es = fmaxf(ea_head / qmax_e, ORC_EPS);
         const float inv_e = 1.0f / es;
         for (int r = 0; r < V; ++r) {
-          const float* e = ebuf + (int64_t)r * K;
+          const float* e = ebuf + (int64_t)r * KP;
           int8_t* erow_w = er_w + (int64_t)r * RK;
           for (int j = 0; j < K; ++j) codes[j] = (int)quant_code(e[j], es, inv_e, qmax_e, mode);
           if (resid_fmt == 1) {

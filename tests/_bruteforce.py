@@ -91,6 +91,12 @@ def packed_decode(mixed, a, b, A_log, dt_bias, scale, sc, ss, rc, rs, idx, H, *,
     """One vLLM-layout step on copies of the pool; returns (out, sc, ss, rc, rs)."""
     sc, ss, rc, rs = sc.copy(), ss.copy(), rc.copy(), rs.copy()
     S, HV, V, K = sc.shape
+    # quantized_packed_decode.py:123-127,158,165-166,196-202: lanes o_k < BK
+    # load 0 past K; the sums run over KP = max(16, next_pow2(K)) values
+    KP = 16
+    while KP < K:
+        KP *= 2
+    Z = [F(0.0)] * (KP - K)
     B = mixed.shape[0]
     qmax = F(2 ** (bits - 1) - 1)
     qe = F(7.0 if resid_fmt == oracle.RESID_INT4 else 127.0)
@@ -102,8 +108,8 @@ def packed_decode(mixed, a, b, A_log, dt_bias, scale, sc, ss, rc, rs, idx, H, *,
             if slot <= 0:
                 continue
             hq = hv // (HV // H)
-            q = [F(mixed[n, hq * K + j]) for j in range(K)]
-            k = [F(mixed[n, H * K + hq * K + j]) for j in range(K)]
+            q = [F(mixed[n, hq * K + j]) for j in range(K)] + Z
+            k = [F(mixed[n, H * K + hq * K + j]) for j in range(K)] + Z
             if l2norm:
                 dq = F(np.sqrt(F(chunk_dot(q, q, 16) + F(1e-6))))
                 dk = F(np.sqrt(F(chunk_dot(k, k, 16) + F(1e-6))))
@@ -114,27 +120,29 @@ def packed_decode(mixed, a, b, A_log, dt_bias, scale, sc, ss, rc, rs, idx, H, *,
             es_head = F(rs[slot, hv]) if per_head else None
             eall = []
             for r in range(V):
+                codes_in = [int(sc[slot, hv, r, j]) for j in range(K)] + [0] * (KP - K)
                 if exact:
-                    h = [F(F(F(int(sc[slot, hv, r, j])) * ss[slot, hv, r]) * al) for j in range(K)]
+                    h = [F(F(F(x) * ss[slot, hv, r]) * al) for x in codes_in]
                 else:
                     sa = F(ss[slot, hv, r] * al)
-                    h = [F(F(int(sc[slot, hv, r, j])) * sa) for j in range(K)]
+                    h = [F(F(x) * sa) for x in codes_in]
                 rd = chunk_dot(h, k, 16)
                 dv = F(be * F(F(mixed[n, 2 * H * K + hv * V + r]) - rd))
-                h = [madd(k[j], dv, h[j], exact) for j in range(K)]
+                h = [madd(k[j], dv, h[j], exact) for j in range(KP)]
                 out[n, hv, r] = chunk_dot(h, q, 16)
                 es_in = es_head if per_head else F(rs[slot, hv, r])
                 if resid_fmt == oracle.RESID_INT4:
                     ec = [nibble(rc[slot, hv, r, j // 2], j) for j in range(K)]
                 else:
                     ec = [int(rc[slot, hv, r, j]) for j in range(K)]
-                t = [madd(F(ec[j]), es_in, h[j], exact) for j in range(K)]
+                ec += [0] * (KP - K)
+                t = [madd(F(ec[j]), es_in, h[j], exact) for j in range(KP)]
                 am = max(abs(x) for x in t)
                 s = F(max(F(am / qmax), F(1e-12)))
                 inv = F(F(1.0) / s)
                 codes = [quant(x, s, inv, qmax, exact) for x in t]
-                e = [resid(t[j], codes[j], s, exact) for j in range(K)]
-                sc[slot, hv, r, :] = np.array(codes, np.int8)
+                e = [resid(t[j], codes[j], s, exact) for j in range(KP)]
+                sc[slot, hv, r, :] = np.array(codes[:K], np.int8)
                 ss[slot, hv, r] = s
                 eall.append(e)
             rows = range(V)
@@ -146,7 +154,7 @@ def packed_decode(mixed, a, b, A_log, dt_bias, scale, sc, ss, rc, rs, idx, H, *,
             for r in rows:
                 es = es_rows[r]
                 inv_e = F(F(1.0) / es)
-                ecodes = [int(quant(x, es, inv_e, qe, exact)) for x in eall[r]]
+                ecodes = [int(quant(x, es, inv_e, qe, exact)) for x in eall[r][:K]]
                 if resid_fmt == oracle.RESID_INT4:
                     for j in range(0, K, 2):        # quantized_packed_decode.py:226-230
                         byte = (ecodes[j] & 0xF) | ((ecodes[j + 1] & 0xF) << 4)

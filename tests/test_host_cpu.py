@@ -55,7 +55,8 @@ def _pd_args(**over):
 
 
 @pytest.mark.parametrize("over,status,msg", [
-    (dict(K=24), _native.CK_EUNSUPPORTED, "K must be one of"),
+    (dict(K=300), _native.CK_EUNSUPPORTED, "K must be at most 256"),
+    (dict(K=25), _native.CK_EINVAL, "even K"),
     (dict(HV=3, H=2), _native.CK_EINVAL, "multiple of H"),
     (dict(qkv_dtype=7), _native.CK_EINVAL, "dtype"),
     (dict(resid_fmt=5), _native.CK_EINVAL, "resid_fmt"),
@@ -64,8 +65,7 @@ def _pd_args(**over):
     (dict(bits=9), _native.CK_EINVAL, "state_bits"),
     (dict(num_slots=0), _native.CK_EINVAL, "num_slots"),
     (dict(mixed=None), _native.CK_EINVAL, "null pointer"),
-    (dict(state=ctypes.c_void_p(17)), _native.CK_EINVAL, "16-byte aligned"),
-    (dict(stride_state=-1), _native.CK_EINVAL, "aligned"),
+    (dict(stride_state=-1), _native.CK_EUNSUPPORTED, "strides must be"),
 ])
 def test_packed_decode_argument_errors(L, over, status, msg):
     rc = L.ck_gdn_packed_decode(*_pd_args(**over))
@@ -146,10 +146,24 @@ def test_qpd_value_errors(mutate, msg):
         qpd.quantized_gated_delta_rule_packed_decode(**c)
 
 
-def test_qpd_unsupported_k():
-    c = _cpu_case(K=48, resid_fmt=qpd.RESID_INT8)
-    with pytest.raises(ValueError, match="packed decode supports K"):
+def test_qpd_k_limits():
+    """K above 256 is refused; an odd K cannot hold an int4 residual (two
+    codes per byte: the reference's packing check, quantized_packed_decode.py:
+    278-281, fires before its even-K check at :306-307, which the C ABI keeps);
+    any other K is accepted and, on CPU tensors, stops at the missing GPU (no
+    host path)."""
+    c = _cpu_case(K=264, resid_fmt=qpd.RESID_INT8)
+    with pytest.raises(ValueError, match="packed decode supports K <= 256"):
         qpd.quantized_gated_delta_rule_packed_decode(**c)
+    c = _cpu_case(K=24, resid_fmt=qpd.RESID_INT4)
+    c.update(mixed_qkv=torch.zeros(2, 2 * 2 * 25 + 4 * 32),
+             state_codes=torch.zeros(3, 4, 32, 25, dtype=torch.int8),
+             resid_codes=torch.zeros(3, 4, 32, 12, dtype=torch.int8))
+    with pytest.raises(ValueError, match="packed two codes per byte"):
+        qpd.quantized_gated_delta_rule_packed_decode(**c)
+    for K, fmt in ((48, qpd.RESID_INT8), (7, qpd.RESID_INT8), (100, qpd.RESID_INT4)):
+        with pytest.raises(_native.HipUnavailable):
+            qpd.quantized_gated_delta_rule_packed_decode(**_cpu_case(K=K, resid_fmt=fmt))
 
 
 def test_qpd_no_cpu_fallback():

@@ -144,6 +144,76 @@ def test_packed_decode_matches_bruteforce(resid_fmt, per_head, exact, l2norm, bi
         np.testing.assert_array_equal(g, r)
 
 
+@pytest.mark.parametrize("K,resid_fmt,exact", [(7, oracle.RESID_INT8, False), (24, oracle.RESID_INT4, True),
+                                               (24, oracle.RESID_INT8, False), (2, oracle.RESID_INT4, False),
+                                               (100, oracle.RESID_INT8, True), (200, oracle.RESID_INT4, False)])
+@pytest.mark.parametrize("per_head", [False, True])
+def test_packed_decode_any_k_matches_bruteforce(K, resid_fmt, exact, per_head):
+    """K that is not a power of two from 16: the brute force pads q, k and
+    every row with zeros to the reference's power-of-two lane count, as its
+    masked loads do (quantized_packed_decode.py:123-127,158,165-166)."""
+    B, H, HV, V = 2, 1, 2, 3
+    pool = make_pool(4, HV, V, K, resid_fmt, per_head, seed=K, bits=8)
+    mixed, a, b, A_log, dt = (x.numpy() for x in make_packed_inputs(B, H, HV, K, V, seed=K + 1))
+    idx = np.array([3, 1], np.int32)
+    ref = bf.packed_decode(mixed, a, b, A_log, dt, 0.5, *pool, idx, H, l2norm=True, resid_fmt=resid_fmt,
+                           per_head=per_head, bits=8, exact=exact)
+    got_pool = [x.copy() for x in pool]
+    out = oracle.packed_decode(mixed, a, b, A_log, dt, 0.5, *got_pool, idx, H, use_qk_l2norm=True,
+                               resid_fmt=resid_fmt, per_head=per_head,
+                               mode=oracle.MODE_EXACT if exact else oracle.MODE_FAST)
+    np.testing.assert_array_equal(out, ref[0])
+    for g, r in zip(got_pool, ref[1:]):
+        np.testing.assert_array_equal(g, r)
+
+
+def _pad_k(pool, mixed, H, HV, V, K, KP, resid_fmt):
+    """The same step posed on rows of KP columns: zero state and residual
+    codes past K, q and k of every head zero-padded to KP."""
+    sc, ss, rc, rs = pool
+    scp = np.zeros(sc.shape[:3] + (KP,), np.int8)
+    scp[..., :K] = sc
+    rk, rkp = (K // 2, KP // 2) if resid_fmt == oracle.RESID_INT4 else (K, KP)
+    rcp = np.zeros(rc.shape[:3] + (rkp,), np.int8)
+    rcp[..., :rk] = rc
+    B = mixed.shape[0]
+    q = np.zeros((B, H, KP), np.float32)
+    k = np.zeros((B, H, KP), np.float32)
+    q[..., :K] = mixed[:, :H * K].reshape(B, H, K)
+    k[..., :K] = mixed[:, H * K:2 * H * K].reshape(B, H, K)
+    mixed_p = np.concatenate([q.reshape(B, -1), k.reshape(B, -1), mixed[:, 2 * H * K:]], axis=1)
+    return (scp, ss.copy(), rcp, rs.copy()), np.ascontiguousarray(mixed_p)
+
+
+@pytest.mark.parametrize("K,KP", [(7, 16), (24, 32), (100, 128), (130, 256)])
+@pytest.mark.parametrize("resid_fmt", [oracle.RESID_INT8, oracle.RESID_INT4])
+@pytest.mark.parametrize("per_head", [False, True])
+@pytest.mark.parametrize("mode", [oracle.MODE_FAST, oracle.MODE_EXACT])
+def test_any_k_step_equals_zero_padded_power_of_two(K, KP, resid_fmt, per_head, mode):
+    """The oracle's any-K step against its power-of-two path on the same rows
+    padded with zero columns (the reference's masked lanes): identical
+    outputs, scales and first K codes, and the padding columns stay zero."""
+    if resid_fmt == oracle.RESID_INT4 and K % 2:
+        pytest.skip("the int4 residual needs an even K")
+    B, H, HV, V = 3, 2, 4, 20
+    pool = make_pool(5, HV, V, K, resid_fmt, per_head, seed=K, bits=8)
+    mixed, a, b, A_log, dt = (x.numpy() for x in make_packed_inputs(B, H, HV, K, V, seed=KP))
+    padded, mixed_p = _pad_k(pool, mixed, H, HV, V, K, KP, resid_fmt)
+    idx = np.array([4, 0, 2], np.int32)
+    for l2norm in (False, True):
+        out = oracle.packed_decode(mixed, a, b, A_log, dt, 0.3, *pool, idx, H, use_qk_l2norm=l2norm,
+                                   resid_fmt=resid_fmt, per_head=per_head, mode=mode)
+        out_p = oracle.packed_decode(mixed_p, a, b, A_log, dt, 0.3, *padded, idx, H, use_qk_l2norm=l2norm,
+                                     resid_fmt=resid_fmt, per_head=per_head, mode=mode)
+        np.testing.assert_array_equal(out, out_p)
+        rk = K // 2 if resid_fmt == oracle.RESID_INT4 else K
+        np.testing.assert_array_equal(pool[0], padded[0][..., :K])
+        np.testing.assert_array_equal(pool[2], padded[2][..., :rk])
+        assert not padded[0][..., K:].any() and not padded[2][..., rk:].any()
+        np.testing.assert_array_equal(pool[1], padded[1])
+        np.testing.assert_array_equal(pool[3], padded[3])
+
+
 @pytest.mark.parametrize("res_fmt", [oracle.RES_FP32, oracle.RES_FP16, oracle.RES_FP8, oracle.RES_INT8])
 @pytest.mark.parametrize("exact", [False, True])
 @pytest.mark.parametrize("HV,K,V", [(2, 16, 4), (1, 64, 5), (1, 256, 3)])
