@@ -22,17 +22,29 @@ pytestmark = pytest.mark.gpu
 DTYPES = (torch.float32, torch.bfloat16, torch.float16)
 
 
-def _draw(seed):
+def _draw(seed, any_k=False):
+    """A random decode configuration. any_k: K anywhere in 1..256 (even with
+    the int4 residual), the masked kernel's shapes."""
     rng = np.random.default_rng(seed)
-    K = int(rng.choice([16, 32, 64, 128, 256]))
+    if any_k:
+        resid_fmt = int(rng.choice([qpd.RESID_INT8, qpd.RESID_INT4]))
+        K = int(rng.integers(1, 257))
+        if resid_fmt == qpd.RESID_INT4 and K % 2:
+            K += 1 if K < 256 else -1
+    else:
+        K = int(rng.choice([16, 32, 64, 128, 256]))
+    KP = 16
+    while KP < K:
+        KP *= 2
     per_head = bool(rng.integers(2))
-    rows_per_inst = 64 // (K // 16)
+    rows_per_inst = 64 // (KP // 16)
     v_max = rows_per_inst * 32 if per_head else 300      # the per-head shapes hold the head in one workgroup
     V = int(rng.integers(1, min(v_max, 300) + 1))
     H = int(rng.choice([1, 2, 4]))
     HV = H * int(rng.choice([1, 2, 3]))
     B = int(rng.integers(1, 25))
-    resid_fmt = int(rng.choice([qpd.RESID_INT8, qpd.RESID_INT4]))
+    if not any_k:
+        resid_fmt = int(rng.choice([qpd.RESID_INT8, qpd.RESID_INT4]))
     mode = "exact" if rng.random() < 0.3 else "fast"
     act = DTYPES[int(rng.integers(3))]
     out_dt = DTYPES[int(rng.integers(3))]
@@ -51,7 +63,17 @@ def _expected_out(o_ref, out_dt):
 
 @pytest.mark.parametrize("seed", range(48))
 def test_random_configuration_bit_exact(device, seed):
-    c = _draw(1000 + seed)
+    _run_decode(device, seed, _draw(1000 + seed))
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_any_k_configuration_bit_exact(device, seed):
+    """K drawn from 1..256: the masked kernel (and, when the draw is a power
+    of two from 16, the bandwidth kernel)."""
+    _run_decode(device, seed, _draw(7000 + seed, any_k=True))
+
+
+def _run_decode(device, seed, c):
     rng = c.pop("rng")
     B, H, HV, K, V = c["B"], c["H"], c["HV"], c["K"], c["V"]
     S = 2 * B + 3 if c["dst"] else B + 3
