@@ -38,6 +38,9 @@ HIPCC_FLAGS = [
     "-ffp-contract=off",
     "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # the bandwidth decode kernel's 12 leading scalar arguments (launch
+    # geometry) go to SGPRs at dispatch
+    "-mllvm", "-amdgpu-kernarg-preload-count=12",
     "-Wall",
     "-Wno-unused-function",
 ]

@@ -175,7 +175,8 @@ void float_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx) 
   const int wave = threadIdx.x >> 6;
   const int c = lane % L::LPR;
   const int g = lane / L::LPR;
-  const pd::WorkSeq w = pd::work_seq(p.items, p.cu_share_n, p.cu_shares);
+  const pd::Geom gm = pd::geom_of(p);
+  const pd::WorkSeq w = pd::work_seq(gm.items, gm.share_n, gm.shares, gm.grid);
   if (w.count <= 0) return;  // whole workgroup
   int item = w.first;
   const int last = p.items - 1;
@@ -183,14 +184,14 @@ void float_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx) 
   // q/k staging buffers alternate between consecutive live items (see
   // packed_decode_kernel)
   FloatItemRegs<RPL, L::QKT, BF16> A, B;
-  ItemCoord ca = pd::item_coord(p, idx, nullptr, item), cb;
+  ItemCoord ca = pd::item_coord(p, gm, idx, nullptr, item), cb;
   load_fitem<K, RPL, WAVES, BF16, ACT>(p, ca, true, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, A);
   float alpha_v, beta_v;
-  pd::gates_for_items(p, w, 0, lane, alpha_v, beta_v);
+  pd::gates_for_items(p, gm, w, 0, lane, alpha_v, beta_v);
   int k = 0, live = 0;
   for (;;) {
     int next = item + w.step;
-    cb = pd::item_coord(p, idx, nullptr, min(next, last));
+    cb = pd::item_coord(p, gm, idx, nullptr, min(next, last));
     load_fitem<K, RPL, WAVES, BF16, ACT>(p, cb, next < item_end, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, B);
     process_fitem<K, RPL, WAVES, BF16, ACT>(p, ca, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, live & 1,
                                             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), k & 63)),
@@ -199,11 +200,11 @@ void float_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx) 
     live += ca.live ? 1 : 0;
     if (next >= item_end) break;
     ++k;
-    if ((k & 63) == 0) pd::gates_for_items(p, w, k, lane, alpha_v, beta_v);
+    if ((k & 63) == 0) pd::gates_for_items(p, gm, w, k, lane, alpha_v, beta_v);
     item = next;
 
     next = item + w.step;
-    ca = pd::item_coord(p, idx, nullptr, min(next, last));
+    ca = pd::item_coord(p, gm, idx, nullptr, min(next, last));
     load_fitem<K, RPL, WAVES, BF16, ACT>(p, ca, next < item_end, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, A);
     process_fitem<K, RPL, WAVES, BF16, ACT>(p, cb, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, live & 1,
                                             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), k & 63)),
@@ -212,7 +213,7 @@ void float_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx) 
     live += cb.live ? 1 : 0;
     if (next >= item_end) break;
     ++k;
-    if ((k & 63) == 0) pd::gates_for_items(p, w, k, lane, alpha_v, beta_v);
+    if ((k & 63) == 0) pd::gates_for_items(p, gm, w, k, lane, alpha_v, beta_v);
     item = next;
   }
 }

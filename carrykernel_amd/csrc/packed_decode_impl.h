@@ -154,23 +154,40 @@ struct ItemCoord {
   bool dlive;     // dslot in [1, num_slots): the update is stored
 };
 
+// Launch geometry: item count, the divisors that split an item number into
+// (request, head, V-tile), the slot-id stride and the item sharing. The
+// bandwidth kernel takes these as its leading scalar arguments, which the
+// compiler preloads into SGPRs (-amdgpu-kernarg-preload-count), so the first
+// slot-id load depends on no kernel-argument load; other kernels read them
+// from PackedParams (geom_of).
+struct Geom {
+  int items, stride_idx, share_n;
+  uint32_t shares;
+  FastDiv nvt, hv;
+  int grid;  // workgroups in the launch (gridDim.x)
+};
+
+__device__ __forceinline__ Geom geom_of(const PackedParams& p) {
+  return Geom{p.items, p.stride_idx, p.cu_share_n, p.cu_shares, p.div_nvt, p.div_hv, (int)gridDim.x};
+}
+
 // Coordinates of an item. `item` is uniform; readfirstlane keeps the results
 // in SGPRs so that the slot id is a scalar load (a vector load here would be
 // ordered behind the prefetch in the vector memory counter).
 // DST: the step writes to the slots in dst_idx (a second scalar load per
 // item); otherwise the destination is the source slot.
 template <bool ONE_TILE = false, bool DST = false>  // ONE_TILE: one V-tile per (request, head), vt = 0
-__device__ __forceinline__ ItemCoord item_coord(const PackedParams& p, const int32_t* __restrict__ idx,
+__device__ __forceinline__ ItemCoord item_coord(const PackedParams& p, const Geom& gm, const int32_t* __restrict__ idx,
                                                 const int32_t* __restrict__ dst_idx, int item) {
   ItemCoord ic;
   item = __builtin_amdgcn_readfirstlane(item);
-  const uint32_t nh = ONE_TILE ? (uint32_t)item : fdiv((uint32_t)item, p.div_nvt);
-  ic.vt = ONE_TILE ? 0 : item - (int)(nh * p.div_nvt.d);
-  const uint32_t n = fdiv(nh, p.div_hv);
-  ic.hv = __builtin_amdgcn_readfirstlane((int)(nh - n * p.div_hv.d));
+  const uint32_t nh = ONE_TILE ? (uint32_t)item : fdiv((uint32_t)item, gm.nvt);
+  ic.vt = ONE_TILE ? 0 : item - (int)(nh * gm.nvt.d);
+  const uint32_t n = fdiv(nh, gm.hv);
+  ic.hv = __builtin_amdgcn_readfirstlane((int)(nh - n * gm.hv.d));
   ic.n = __builtin_amdgcn_readfirstlane((int)n);
   ic.vt = __builtin_amdgcn_readfirstlane(ic.vt);
-  ic.slot = (int64_t)idx[(int64_t)ic.n * p.stride_idx];
+  ic.slot = (int64_t)idx[(int64_t)ic.n * gm.stride_idx];
   ic.live = ic.slot > 0 && ic.slot < p.num_slots;
   if constexpr (DST) {
     ic.dslot = (int64_t)dst_idx[(int64_t)ic.n * p.stride_dst_idx];
@@ -628,8 +645,7 @@ struct WorkSeq {
 // start, where c_a is the sum of the shares (bytes of cu_shares) of the
 // older ages. Any shares are correct (each item is taken exactly once); they
 // only change when the workgroups of a CU finish.
-__device__ __forceinline__ WorkSeq work_seq(int items, int share_n, uint32_t shares) {
-  const int G = (int)gridDim.x;
+__device__ __forceinline__ WorkSeq work_seq(int items, int share_n, uint32_t shares, int G) {
   const int b = (int)blockIdx.x;
   WorkSeq w;
   if (share_n > 1 && G % share_n == 0 && items >= 2 * G) {
@@ -683,15 +699,15 @@ inline void set_cu_shares(PackedParams& p, int grid, int resident, int per_cu) {
 }
 
 // Gates of this workgroup's items number kbase .. kbase+63 (one per lane).
-__device__ __forceinline__ void gates_for_items(const PackedParams& p, const WorkSeq& w, int kbase, int lane,
-                                                float& alpha_v, float& beta_v) {
+__device__ __forceinline__ void gates_for_items(const PackedParams& p, const Geom& gm, const WorkSeq& w, int kbase,
+                                                int lane, float& alpha_v, float& beta_v) {
   // Branch-free over lanes (lanes past the last item recompute the last
   // item's gates, which are never read): a divergent region here would move
   // the uniform dtype/stride values into VGPRs that stay live over the loop.
-  const int item = min(w.first + (kbase + lane) * w.step, p.items - 1);
-  const uint32_t nh = fdiv((uint32_t)item, p.div_nvt);
-  const uint32_t n = fdiv(nh, p.div_hv);
-  const int hv = (int)(nh - n * p.div_hv.d);
+  const int item = min(w.first + (kbase + lane) * w.step, gm.items - 1);
+  const uint32_t nh = fdiv((uint32_t)item, gm.nvt);
+  const uint32_t n = fdiv(nh, gm.hv);
+  const int hv = (int)(nh - n * gm.hv.d);
   // all four loads are issued before any value is decoded: a conversion next
   // to its load would wait for every load in flight (including the items')
   const ActBits ra = load_act_bits(p.a, (int64_t)n * p.stride_a + hv, p.a_dtype());
@@ -710,8 +726,11 @@ constexpr int kMinWavesPerEU = (RPL == 2 && (WAVES == 8 || WAVES == 4)) ? 4 : 1;
 
 template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ACT, bool DST>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(kMinWavesPerEU<RPL, WAVES>)))
-void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx, const int32_t* __restrict__ dst_idx) {
+void packed_decode_kernel(const int32_t* __restrict__ idx, int items, int stride_idx, uint32_t nvt_d, uint32_t nvt_m,
+                          uint32_t nvt_sh, uint32_t hv_d, uint32_t hv_m, uint32_t hv_sh, int share_n, uint32_t shares,
+                          int grid, const PackedParams p, const int32_t* __restrict__ dst_idx) {
   using L = Layout<K, RPL, WAVES, RESID, PER_HEAD>;
+  const Geom gm{items, stride_idx, share_n, shares, FastDiv{nvt_d, nvt_m, nvt_sh}, FastDiv{hv_d, hv_m, hv_sh}, grid};
   __shared__ __attribute__((aligned(16))) float s_qk[4][2 * K];  // [parity] staged, [2 + parity] raw
   __shared__ float s_red[2][WAVES];
   __shared__ float4 s_ek[kResidInLds<RPL, RESID, PER_HEAD> ? WAVES * RPL * 4 * 64 : 1];
@@ -722,17 +741,17 @@ void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx,
   const int g = lane / L::LPR;
   tl_start(p);
 
-  const WorkSeq w = work_seq(p.items, p.cu_share_n, p.cu_shares);
+  const WorkSeq w = work_seq(gm.items, gm.share_n, gm.shares, gm.grid);
   if (w.count <= 0) return;  // whole workgroup
   int item = w.first;
-  const int last = p.items - 1;
+  const int last = gm.items - 1;
   const int item_end = w.first + w.count * w.step;  // one past this workgroup's last item
 
   // LDS buffers alternate between consecutive live items (a NULL item skips
   // the barriers, so the parity follows a count of live items): two uses of
   // one buffer are always separated by the barrier of the live item between.
   ItemRegs<RPL, L::EW, L::QKT> A, B;
-  ItemCoord ca = item_coord<false, DST>(p, idx, dst_idx, item), cb;
+  ItemCoord ca = item_coord<false, DST>(p, gm, idx, dst_idx, item), cb;
 #if CK_TIMELINE
   asm volatile("" ::"s"((int)ca.slot));
   tl_mark(p, 32);
@@ -740,7 +759,7 @@ void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx,
   load_item<K, RPL, WAVES, RESID, PER_HEAD, ACT>(p, ca, true, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, A);
   tl_mark(p, 33);
   float alpha_v, beta_v;
-  gates_for_items(p, w, 0, lane, alpha_v, beta_v);  // its loads overlap the first item's
+  gates_for_items(p, gm, w, 0, lane, alpha_v, beta_v);  // its loads overlap the first item's
 #if CK_TIMELINE
   asm volatile("" ::"v"(alpha_v), "v"(beta_v));
   tl_mark(p, 34);
@@ -750,7 +769,7 @@ void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx,
   for (;;) {
     // ---- item k in A; prefetch item k+1 into B (past the end: re-read the last item) ----
     int next = item + w.step;
-    cb = item_coord<false, DST>(p, idx, dst_idx, min(next, last));
+    cb = item_coord<false, DST>(p, gm, idx, dst_idx, min(next, last));
     load_item<K, RPL, WAVES, RESID, PER_HEAD, ACT>(p, cb, next < item_end, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, B);
     {
       const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), k & 63));
@@ -764,12 +783,12 @@ void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx,
     }
     if (next >= item_end) break;
     ++k;
-    if ((k & 63) == 0) gates_for_items(p, w, k, lane, alpha_v, beta_v);
+    if ((k & 63) == 0) gates_for_items(p, gm, w, k, lane, alpha_v, beta_v);
     item = next;
 
     // ---- item k in B; prefetch item k+1 into A ----
     next = item + w.step;
-    ca = item_coord<false, DST>(p, idx, dst_idx, min(next, last));
+    ca = item_coord<false, DST>(p, gm, idx, dst_idx, min(next, last));
     load_item<K, RPL, WAVES, RESID, PER_HEAD, ACT>(p, ca, next < item_end, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, A);
     {
       const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), k & 63));
@@ -783,7 +802,7 @@ void packed_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx,
     }
     if (next >= item_end) break;
     ++k;
-    if ((k & 63) == 0) gates_for_items(p, w, k, lane, alpha_v, beta_v);
+    if ((k & 63) == 0) gates_for_items(p, gm, w, k, lane, alpha_v, beta_v);
     item = next;
   }
 }
@@ -810,7 +829,9 @@ int launch_cfg(PackedParams p, int B, hipStream_t stream) {
   const int per_wg = (p.items + resident - 1) / resident;
   const int grid = (p.items + per_wg - 1) / per_wg;
   set_cu_shares(p, grid, resident, per_cu);
-  hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(WAVES * 64), 0, stream, p, p.idx, p.dst_idx);
+  hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(WAVES * 64), 0, stream, p.idx, p.items, p.stride_idx, p.div_nvt.d,
+                     p.div_nvt.m, p.div_nvt.sh, p.div_hv.d, p.div_hv.m, p.div_hv.sh, p.cu_share_n, p.cu_shares, grid,
+                     p, p.dst_idx);
   return check_launch("ck_gdn_packed_decode");
 }
 

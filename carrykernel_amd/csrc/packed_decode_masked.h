@@ -104,7 +104,8 @@ __global__ __launch_bounds__(WAVES * 64) void packed_decode_masked_kernel(const 
   const int c = lane % L::LPR;
   const int g = lane / L::LPR;
   const int item = (int)blockIdx.x;
-  const ItemCoord ic = item_coord<false, DST>(p, idx, dst_idx, item);
+  const Geom gm = geom_of(p);
+  const ItemCoord ic = item_coord<false, DST>(p, gm, idx, dst_idx, item);
   const int row0 = ic.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g;
   ItemRegs<RPL, L::EW, L::QKT> R{};
   if (ic.live) load_item_masked<KP, RPL, WAVES, RESID, PER_HEAD, MASK>(p, ic, row0, c, R);
@@ -112,7 +113,7 @@ __global__ __launch_bounds__(WAVES * 64) void packed_decode_masked_kernel(const 
   // gates of the following items, which are not used)
   const WorkSeq w{item, 1, 1};
   float alpha_v, beta_v;
-  gates_for_items(p, w, 0, lane, alpha_v, beta_v);
+  gates_for_items(p, gm, w, 0, lane, alpha_v, beta_v);
   const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), 0));
   const float beta = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(beta_v), 0));
   process_item<KP, RPL, WAVES, RESID, PER_HEAD, MODE, kF32, DST, MASK>(p, ic, row0, c, lane, wave, 0, alpha, beta,
