@@ -1035,6 +1035,7 @@ def main():
         cases = [(bb, f, "fast") for bb in (1, 8, 64, 256) for f in formats] + [(128, "int4_row", "fast")]
     else:
         cases = [(bb, "int4_head", "fast") for bb in (1, 8, 256)] + [(8, "int8_head", "fast"),
+                                                                      (1, "int4_row", "fast"),
                                                                       (128, "int4_row", "fast")]
     if not args.no_sweep:
         cases += [(64, "int4_head", "exact"), (256, "int4_head", "exact")]

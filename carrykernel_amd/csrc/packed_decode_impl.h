@@ -838,7 +838,11 @@ int launch_cfg(PackedParams p, int B, hipStream_t stream) {
 // Workgroup shape (numbers for K=128, where a lane row is 16 K and a wave
 // instruction covers 8 rows). With per-row residual scales a workgroup is 4
 // waves of 2 rows per lane (64-row tiles, four workgroups per CU) when that
-// gives 512 tiles or more, else 1 wave of 4 rows per lane (32-row tiles). A
+// gives 512 tiles or more, else 4 waves of 1 row per lane (32-row tiles): a
+// small batch's rows then spread over four times as many SIMDs, each wave
+// computing a quarter of what one wave of 4 rows per lane would (B=1 to 4 at
+// HV=32: 6.5 / 6.6 / 7.3 us -> 4.7 / 4.7 / 5.7 us; from B=8 the 64-row tiles
+// are faster). A
 // per-head residual scale needs the whole head in one workgroup; at K=128 that
 // is 8 waves of 2 rows per lane, which fits 128 VGPRs (the int8 residual's
 // unquantized values wait for the head amax in LDS) and so two workgroups per
@@ -849,7 +853,7 @@ int launch_k(const PackedParams& p, int B, hipStream_t stream) {
   if constexpr (!PER_HEAD) {
     if ((int64_t)B * p.HV * ((p.V + RPI * 8 - 1) / (RPI * 8)) >= 512)
       return launch_cfg<K, 2, 4, RESID, false, MODE, ACT, DST>(p, B, stream);
-    return launch_cfg<K, 4, 1, RESID, false, MODE, ACT, DST>(p, B, stream);
+    return launch_cfg<K, 1, 4, RESID, false, MODE, ACT, DST>(p, B, stream);
   } else {
     const int need = p.V;
     if constexpr (K == 128) {
