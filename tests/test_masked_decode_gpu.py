@@ -45,6 +45,9 @@ CASES = {
                                   False),
     "k192_int4_row_lanes_out_of_place": (192, 6, 2, 4, 128, I4, False, "fast", F16, F32, True, 0.0, False, True, 8,
                                          2, False),
+    # 64 x 8 x 4 = 2048 tiles of 32 rows: the one-wave, 4-rows-per-lane shape
+    "k96_int4_row_lanes_many_tiles": (96, 64, 2, 8, 128, I4, False, "fast", F32, F32, True, 0.1, True, False, 8, 2,
+                                      False),
     "k240_int8_head_lanes": (240, 3, 1, 3, 100, I8, True, "fast", F32, F32, False, 0.0, False, False, 6, 2, False),
     "k128_misaligned_int4_head": (128, 8, 4, 8, 128, I4, True, "fast", F32, F32, True, 0.1, True, False, 8, 2,
                                   True),
