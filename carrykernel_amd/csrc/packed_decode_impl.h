@@ -846,7 +846,8 @@ int launch_cfg(PackedParams p, int B, hipStream_t stream) {
 // per-head residual scale needs the whole head in one workgroup; at K=128 that
 // is 8 waves of 2 rows per lane, which fits 128 VGPRs (the int8 residual's
 // unquantized values wait for the head amax in LDS) and so two workgroups per
-// CU; other K keep 4 rows per lane.
+// CU; K=64, 32 and 16 spread a 128-row head over more waves (below); other
+// shapes keep 4 rows per lane.
 template <int K, int RESID, bool PER_HEAD, int MODE, int ACT, bool DST>
 int launch_k(const PackedParams& p, int B, hipStream_t stream) {
   constexpr int RPI = 64 / (K / 16);
@@ -858,6 +859,20 @@ int launch_k(const PackedParams& p, int B, hipStream_t stream) {
     const int need = p.V;
     if constexpr (K == 128) {
       if (need > RPI * 4 * 2 && need <= RPI * 2 * 8) return launch_cfg<K, 2, 8, RESID, true, MODE, ACT, DST>(p, B, stream);
+    }
+    // fewer rows per lane over more waves for a V=128 head at small K (per-head,
+    // int4, HV=32, us at B=1 / 64): K=64 2 rows x 4 waves 6.9 / 16.1 -> 5.7 /
+    // 14.8; K=16 1 row x 2 waves 6.2 / 9.2 -> 4.9 / 8.7; K=32 1 row x 4 waves
+    // 6.5 -> 5.0 at B=1 but 10.3 -> 11.9 at B=64, so only up to one item per CU
+    if constexpr (K == 64) {
+      if (need > RPI * 4 * 1 && need <= RPI * 2 * 4) return launch_cfg<K, 2, 4, RESID, true, MODE, ACT, DST>(p, B, stream);
+    }
+    if constexpr (K == 32) {
+      if (need > RPI * 2 && need <= RPI * 4 && (int64_t)B * p.HV <= 256)
+        return launch_cfg<K, 1, 4, RESID, true, MODE, ACT, DST>(p, B, stream);
+    }
+    if constexpr (K == 16) {
+      if (need > RPI && need <= RPI * 2) return launch_cfg<K, 1, 2, RESID, true, MODE, ACT, DST>(p, B, stream);
     }
     if (need <= RPI * 4 * 1) return launch_cfg<K, 4, 1, RESID, true, MODE, ACT, DST>(p, B, stream);
     if (need <= RPI * 4 * 2) return launch_cfg<K, 4, 2, RESID, true, MODE, ACT, DST>(p, B, stream);

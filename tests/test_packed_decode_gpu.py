@@ -81,6 +81,17 @@ def test_bit_exact_shapes(device, K, V, H, HV, resid_fmt, per_head):
               mode="fast", l2norm=True, T=2, seed=K + V)
 
 
+@pytest.mark.parametrize("K,B,HV", [(64, 3, 8), (32, 3, 8), (32, 9, 32), (16, 3, 8)])
+@pytest.mark.parametrize("resid_fmt", [qpd.RESID_INT8, qpd.RESID_INT4])
+@pytest.mark.parametrize("mode", ["fast", "exact"])
+def test_bit_exact_small_k_per_head_shapes(device, K, B, HV, resid_fmt, mode):
+    """A V=128 head at K = 64 / 32 / 16 with a per-head residual scale: 2 rows
+    per lane over 4 waves, 1 row over 4 waves (up to 256 items; B=9 x HV=32
+    takes the one-wave shape) and 1 row over 2 waves."""
+    _run_both(device, B=B, H=HV // 2, HV=HV, K=K, V=128, resid_fmt=resid_fmt, per_head=True,
+              mode=mode, l2norm=True, T=2, seed=K + B)
+
+
 @pytest.mark.parametrize("act_dtype,out_dtype", [(torch.bfloat16, torch.bfloat16),
                                                  (torch.float16, torch.float32),
                                                  (torch.float32, torch.bfloat16)])
