@@ -171,6 +171,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
 void float_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx) {
   using L = FLayout<K, RPL, WAVES>;
   __shared__ __attribute__((aligned(16))) float s_qk[4][2 * K];  // [parity] staged, [2 + parity] raw
+  __shared__ float2 s_gate[pd::kGateCap];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int c = lane % L::LPR;
@@ -186,34 +187,30 @@ void float_decode_kernel(const PackedParams p, const int32_t* __restrict__ idx) 
   FloatItemRegs<RPL, L::QKT, BF16> A, B;
   ItemCoord ca = pd::item_coord(p, gm, idx, nullptr, item), cb;
   load_fitem<K, RPL, WAVES, BF16, ACT>(p, ca, true, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, A);
-  float alpha_v, beta_v;
-  pd::gates_for_items(p, gm, w, 0, lane, alpha_v, beta_v);
+  pd::stage_gates<WAVES, true>(p, gm, w, wave, lane, s_gate);
   int k = 0, live = 0;
   for (;;) {
     int next = item + w.step;
     cb = pd::item_coord(p, gm, idx, nullptr, min(next, last));
     load_fitem<K, RPL, WAVES, BF16, ACT>(p, cb, next < item_end, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, B);
-    process_fitem<K, RPL, WAVES, BF16, ACT>(p, ca, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, live & 1,
-                                            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), k & 63)),
-                                            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(beta_v), k & 63)),
-                                            A, s_qk);
+    if (k == 0) __syncthreads();  // the staged gates are visible from here on
+    float2 gab = s_gate[min(k, pd::kGateCap - 1)];
+    process_fitem<K, RPL, WAVES, BF16, ACT>(p, ca, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, live & 1, gab.x,
+                                            gab.y, A, s_qk);
     live += ca.live ? 1 : 0;
     if (next >= item_end) break;
     ++k;
-    if ((k & 63) == 0) pd::gates_for_items(p, gm, w, k, lane, alpha_v, beta_v);
     item = next;
 
     next = item + w.step;
     ca = pd::item_coord(p, gm, idx, nullptr, min(next, last));
     load_fitem<K, RPL, WAVES, BF16, ACT>(p, ca, next < item_end, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, A);
-    process_fitem<K, RPL, WAVES, BF16, ACT>(p, cb, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, live & 1,
-                                            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), k & 63)),
-                                            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(beta_v), k & 63)),
-                                            B, s_qk);
+    gab = s_gate[min(k, pd::kGateCap - 1)];
+    process_fitem<K, RPL, WAVES, BF16, ACT>(p, cb, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, live & 1, gab.x,
+                                            gab.y, B, s_qk);
     live += cb.live ? 1 : 0;
     if (next >= item_end) break;
     ++k;
-    if ((k & 63) == 0) pd::gates_for_items(p, gm, w, k, lane, alpha_v, beta_v);
     item = next;
   }
 }
@@ -233,6 +230,17 @@ int launch_fs(PackedParams p, int B, hipStream_t stream) {
   int per_cu = 0;
   const int resident = pd::resident_workgroups(reinterpret_cast<const void*>(fn), WAVES * 64, &per_cu);
   if (resident <= 0) return fail(CK_ELAUNCH, "cannot query the device occupancy");
+  const int64_t cap = pd::launch_item_cap(resident, per_cu);
+  if (items > cap) {  // consecutive launches over slices of the requests
+    const int64_t per_request = (int64_t)p.HV * nvt;
+    if (per_request > cap) return fail(CK_EUNSUPPORTED, "%lld work items per request is too many", (long long)per_request);
+    const int chunk = (int)(cap / per_request);
+    for (int n0 = 0; n0 < B; n0 += chunk) {
+      const int rc = launch_fs<K, BF16, ACT>(pd::requests_from(p, n0), min(chunk, B - n0), stream);
+      if (rc != CK_OK) return rc;
+    }
+    return ok();
+  }
   const int per_wg = (p.items + resident - 1) / resident;
   const int grid = (p.items + per_wg - 1) / per_wg;
   pd::set_cu_shares(p, grid, resident, per_cu);

@@ -40,6 +40,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
+
 #include "ck_capi_common.h"
 #include "ck_device.h"
 #include "ck_quant.h"
@@ -718,6 +720,69 @@ __device__ __forceinline__ void gates_for_items(const PackedParams& p, const Geo
            decode_act_bits(rd, p.dt_bias_dtype()), &alpha_v, &beta_v);
 }
 
+// Gates (alpha, beta) of every item of a workgroup, computed before its item
+// loop into LDS: chunk v of 64 items goes to wave v (ROTATE: wave v - b mod
+// WAVES in workgroup b), the next to wave v + WAVES, so a workgroup of up to
+// 64 items evaluates them in one wave. Nothing in the item loop refers to the
+// gate inputs, so their pointers, strides and dtype tests are dead there (a
+// refresh of a per-wave gate table inside the loop kept them live and spilled
+// 36 SGPRs to VGPR lanes in the K=128 8-wave kernel). The item loop reads
+// them after a barrier ahead of its first item; the host keeps a launch's
+// items per workgroup at or below kGateCap (launch_item_cap).
+//
+// A wave with no chunk waits here for its first item's loads, as a gate wave
+// does for the gate inputs issued after them (the vector memory counter
+// retires in order), so no wave issues its second item's loads while its
+// first item's are still arriving: at start-up every workgroup of the grid
+// loads at once, and the first items' data then lands earlier (per-head int4,
+// us: B=1 6.3 -> 5.9, B=64 27.0 -> 26.7, B=256 84.8 -> 84.4). Which wave
+// evaluates the gates was measured per shape: the first-dispatched wave for
+// the 8-wave per-head workgroups (rotated: B=1 6.3), rotated for the four
+// 4-wave per-row workgroups of a CU (wave 0 in every one: B=128 47.3 us
+// against 45.5).
+constexpr int kGateCap = 256;
+constexpr int kWaitVmcnt0 = 0x0f70;  // s_waitcnt simm16: vmcnt 0, expcnt 7, lgkmcnt 15 (vector memory only)
+
+template <int WAVES, bool ROTATE>
+__device__ __forceinline__ void stage_gates(const PackedParams& p, const Geom& gm, const WorkSeq& w, int wave,
+                                            int lane, float2* s_gate) {
+  const int n = min(w.count, kGateCap);
+  const int v = ROTATE ? (wave + (int)blockIdx.x) % WAVES : wave;
+  for (int kb = v * 64; kb < n; kb += WAVES * 64) {
+    float a, b;
+    gates_for_items(p, gm, w, kb, lane, a, b);
+    if (kb + lane < n) s_gate[kb + lane] = make_float2(a, b);
+  }
+  if (v * 64 >= n) __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+}
+
+// Items one launch may hold so that no workgroup gets more than kGateCap:
+// a workgroup's items come from one CU group of ceil(items / m) items, m =
+// resident / per_cu (work_seq; the plain stride gives fewer). A positive
+// CARRYKERNEL_MAX_ITEMS_PER_LAUNCH lowers it (tests of the split).
+inline int64_t launch_item_cap(int resident, int per_cu) {
+  int64_t cap = (int64_t)kGateCap * (resident / (per_cu > 1 ? per_cu : 1));
+  if (const char* e = getenv("CARRYKERNEL_MAX_ITEMS_PER_LAUNCH")) {
+    const long long v = atoll(e);
+    if (v > 0 && v < cap) cap = v;
+  }
+  return cap;
+}
+
+// The same step for requests n0 .. of p: per-request inputs, outputs and ids
+// advanced by n0 requests (the pool and the per-head inputs are shared).
+inline PackedParams requests_from(const PackedParams& p, int n0) {
+  auto esz = [](int dt) { return dt == kF32 ? 4 : 2; };
+  PackedParams q = p;
+  q.mixed = static_cast<const char*>(p.mixed) + (int64_t)n0 * p.stride_mixed * esz(p.dtypes & 15);
+  q.a = static_cast<const char*>(p.a) + (int64_t)n0 * p.stride_a * esz((p.dtypes >> 4) & 15);
+  q.b = static_cast<const char*>(p.b) + (int64_t)n0 * p.stride_b * esz((p.dtypes >> 8) & 15);
+  q.out = static_cast<char*>(p.out) + (int64_t)n0 * p.HV * p.V * esz((p.dtypes >> 20) & 15);
+  q.idx = p.idx + (int64_t)n0 * p.stride_idx;
+  if (p.dst_idx) q.dst_idx = p.dst_idx + (int64_t)n0 * p.stride_dst_idx;
+  return q;
+}
+
 // Waves per SIMD the register allocation must allow: two 8-wave or four
 // 4-wave workgroups per CU need 4 (<= 128 VGPRs); other shapes take what they
 // need.
@@ -734,6 +799,7 @@ void packed_decode_kernel(const int32_t* __restrict__ idx, int items, int stride
   __shared__ __attribute__((aligned(16))) float s_qk[4][2 * K];  // [parity] staged, [2 + parity] raw
   __shared__ float s_red[2][WAVES];
   __shared__ float4 s_ek[kResidInLds<RPL, RESID, PER_HEAD> ? WAVES * RPL * 4 * 64 : 1];
+  __shared__ float2 s_gate[kGateCap];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -758,12 +824,8 @@ void packed_decode_kernel(const int32_t* __restrict__ idx, int items, int stride
 #endif
   load_item<K, RPL, WAVES, RESID, PER_HEAD, ACT>(p, ca, true, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, A);
   tl_mark(p, 33);
-  float alpha_v, beta_v;
-  gates_for_items(p, gm, w, 0, lane, alpha_v, beta_v);  // its loads overlap the first item's
-#if CK_TIMELINE
-  asm volatile("" ::"v"(alpha_v), "v"(beta_v));
+  stage_gates<WAVES, !PER_HEAD>(p, gm, w, wave, lane, s_gate);  // its loads overlap the first item's
   tl_mark(p, 34);
-#endif
   int k = 0;     // item number within this workgroup
   int live = 0;  // live items processed so far
   for (;;) {
@@ -772,18 +834,17 @@ void packed_decode_kernel(const int32_t* __restrict__ idx, int items, int stride
     cb = item_coord<false, DST>(p, gm, idx, dst_idx, min(next, last));
     load_item<K, RPL, WAVES, RESID, PER_HEAD, ACT>(p, cb, next < item_end, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, B);
     {
-      const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), k & 63));
-      const float beta = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(beta_v), k & 63));
+      if (k == 0) __syncthreads();  // the staged gates are visible from here on
+      const float2 gab = s_gate[min(k, kGateCap - 1)];
       tl_mark(p, tl_item_slot(k, 0));
       tl_data_ready(p, k, A);
       process_item<K, RPL, WAVES, RESID, PER_HEAD, MODE, ACT, DST>(p, ca, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c,
-                                                          lane, wave, live & 1, alpha, beta, A, s_qk, s_red, s_ek);
+                                                          lane, wave, live & 1, gab.x, gab.y, A, s_qk, s_red, s_ek);
       live += ca.live ? 1 : 0;
       tl_mark(p, tl_item_slot(k, 2));
     }
     if (next >= item_end) break;
     ++k;
-    if ((k & 63) == 0) gates_for_items(p, gm, w, k, lane, alpha_v, beta_v);
     item = next;
 
     // ---- item k in B; prefetch item k+1 into A ----
@@ -791,18 +852,16 @@ void packed_decode_kernel(const int32_t* __restrict__ idx, int items, int stride
     ca = item_coord<false, DST>(p, gm, idx, dst_idx, min(next, last));
     load_item<K, RPL, WAVES, RESID, PER_HEAD, ACT>(p, ca, next < item_end, ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c, A);
     {
-      const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), k & 63));
-      const float beta = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(beta_v), k & 63));
+      const float2 gab = s_gate[min(k, kGateCap - 1)];
       tl_mark(p, tl_item_slot(k, 0));
       tl_data_ready(p, k, B);
       process_item<K, RPL, WAVES, RESID, PER_HEAD, MODE, ACT, DST>(p, cb, cb.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g, c,
-                                                          lane, wave, live & 1, alpha, beta, B, s_qk, s_red, s_ek);
+                                                          lane, wave, live & 1, gab.x, gab.y, B, s_qk, s_red, s_ek);
       live += cb.live ? 1 : 0;
       tl_mark(p, tl_item_slot(k, 2));
     }
     if (next >= item_end) break;
     ++k;
-    if ((k & 63) == 0) gates_for_items(p, gm, w, k, lane, alpha_v, beta_v);
     item = next;
   }
 }
@@ -825,6 +884,18 @@ int launch_cfg(PackedParams p, int B, hipStream_t stream) {
   int per_cu = 0;
   const int resident = resident_workgroups(reinterpret_cast<const void*>(fn), WAVES * 64, &per_cu);
   if (resident <= 0) return fail(CK_ELAUNCH, "cannot query the device occupancy");
+  const int64_t cap = launch_item_cap(resident, per_cu);
+  if (items > cap) {  // consecutive launches over slices of the requests
+    const int64_t per_request = (int64_t)p.HV * nvt;
+    if (per_request > cap) return fail(CK_EUNSUPPORTED, "%lld work items per request is too many", (long long)per_request);
+    const int chunk = (int)(cap / per_request);
+    for (int n0 = 0; n0 < B; n0 += chunk) {
+      const int rc = launch_cfg<K, RPL, WAVES, RESID, PER_HEAD, MODE, ACT, DST>(requests_from(p, n0), min(chunk, B - n0),
+                                                                              stream);
+      if (rc != CK_OK) return rc;
+    }
+    return ok();
+  }
   // fewest items per workgroup, then the fewest workgroups achieving it
   const int per_wg = (p.items + resident - 1) / resident;
   const int grid = (p.items + per_wg - 1) / per_wg;

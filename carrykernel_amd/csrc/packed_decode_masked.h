@@ -98,6 +98,7 @@ __global__ __launch_bounds__(WAVES * 64) void packed_decode_masked_kernel(const 
   __shared__ __attribute__((aligned(16))) float s_qk[4][2 * KP];  // [parity] staged, [2 + parity] raw
   __shared__ float s_red[2][WAVES];
   __shared__ float4 s_ek[kResidInLds<RPL, RESID, PER_HEAD> ? WAVES * RPL * 4 * 64 : 1];
+  __shared__ float2 s_gate[1];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -109,15 +110,12 @@ __global__ __launch_bounds__(WAVES * 64) void packed_decode_masked_kernel(const 
   const int row0 = ic.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g;
   ItemRegs<RPL, L::EW, L::QKT> R{};
   if (ic.live) load_item_masked<KP, RPL, WAVES, RESID, PER_HEAD, MASK>(p, ic, row0, c, R);
-  // the gates of this item come out of lane 0 (the other lanes evaluate the
-  // gates of the following items, which are not used)
-  const WorkSeq w{item, 1, 1};
-  float alpha_v, beta_v;
-  gates_for_items(p, gm, w, 0, lane, alpha_v, beta_v);
-  const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_v), 0));
-  const float beta = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(beta_v), 0));
-  process_item<KP, RPL, WAVES, RESID, PER_HEAD, MODE, kF32, DST, MASK>(p, ic, row0, c, lane, wave, 0, alpha, beta,
-                                                                        R, s_qk, s_red, s_ek);
+  // wave 0 evaluates this item's gates into LDS
+  stage_gates<1, false>(p, gm, WorkSeq{item, 1, 1}, wave, lane, s_gate);
+  __syncthreads();
+  const float2 gab = s_gate[0];
+  process_item<KP, RPL, WAVES, RESID, PER_HEAD, MODE, kF32, DST, MASK>(p, ic, row0, c, lane, wave, 0, gab.x, gab.y, R,
+                                                                        s_qk, s_red, s_ek);
 }
 
 template <int KP, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, bool DST, int MASK>

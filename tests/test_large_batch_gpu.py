@@ -1,13 +1,17 @@
 """GPU runs at the configs' full sizes and at serving batches large enough
-that a workgroup takes more than 64 items (so the per-workgroup gate table
-of 64 items is refilled mid-loop):
+that a workgroup takes more than 64 items (its gates are staged in LDS by
+more than one wave) or that the step is split over consecutive launches
+(more items than a launch may hold):
 
 * C3 at B=256 (HV=32, K=V=128, int4 residual with a per-head scale), two
   steps bit for bit against the oracle;
-* B=1100 through the quantized decode (per-head int4 FAST and per-row int8
-  EXACT) and through the bf16-state arm: every workgroup of the persistent
-  grid runs more than 64 items at this batch, and every item is checked bit
-  for bit;
+* B=1100 through the quantized decode (per-head int4 FAST: one launch,
+  more than 64 items per workgroup; per-row int8 EXACT: 70,400 items, two
+  launches) and through the bf16-state arm (two launches): every item is
+  checked bit for bit;
+* small steps split into launches of a few items (a lowered
+  CARRYKERNEL_MAX_ITEMS_PER_LAUNCH) with bf16 activations and output,
+  strided ids and out-of-place destinations;
 * C5 at full size (24 layers x B=64 x 2048 tokens, int8 and int6 state,
   mixed alpha), its drift against the fp32 state arm bounded and the
   residual lowering the state error at every report.
@@ -78,15 +82,17 @@ def test_c3_b256_bit_exact(device):
 def test_more_than_64_items_per_workgroup(device, resid_fmt, per_head, mode):
     """B=1100 requests x 32 heads: the persistent grid (at most four
     workgroups per CU on 256 CUs) gives every workgroup more than 64 items,
-    so gates of items 64.. come from the refilled table. GQA (H=16), the
-    in-kernel L2 norm, every item checked bit for bit."""
+    so a second wave stages the gates of items 64..; the per-row shape's
+    70,400 items exceed what one launch holds (256 per workgroup), so the
+    requests are split over two launches. GQA (H=16), the in-kernel L2 norm,
+    every item checked bit for bit."""
     B = 1100
     S = B + 1
     cus = torch.cuda.get_device_properties(device).multi_processor_count
     # per-head: one 8-wave workgroup per head item, two per CU; per-row:
     # 64-row items, four 4-wave workgroups per CU
     items, per_cu = (B * HV, 2) if per_head else (B * HV * (V // 64), 4)
-    assert items / (per_cu * cus) > 64, "batch too small to refill the gate table on this device"
+    assert items / (per_cu * cus) > 64, "batch too small for more than 64 items per workgroup on this device"
     Hq = 16
     pool = [torch.from_numpy(x).to(device) for x in make_pool(S, HV, V, K, resid_fmt, per_head, seed=8)]
     inputs = [x.to(device) for x in make_packed_inputs(B, Hq, HV, K, V, seed=8)]
@@ -108,8 +114,8 @@ def test_more_than_64_items_per_workgroup(device, resid_fmt, per_head, mode):
 
 
 def test_float_state_more_than_64_items_per_workgroup(device):
-    """The bf16-state arm at B=1100 (two 64-row items per head): more than 64
-    items per workgroup, every output and state row bit for bit."""
+    """The bf16-state arm at B=1100 (two 64-row items per head, 70,400 items:
+    two launches), every output and state row bit for bit."""
     B = 1100
     S = B + 1
     g = torch.Generator().manual_seed(9)
@@ -144,3 +150,65 @@ def test_c5_full_size_drift(device, bits, bound):
     for r in rows:
         assert r["state_rel"] < bound and r["o_rel"] < bound
         assert r["state_plus_residual_rel"] < r["state_rel"]
+
+
+@pytest.mark.parametrize("per_head,resid_fmt,cap", [(True, oracle.RESID_INT4, 40), (False, oracle.RESID_INT8, 150)])
+def test_split_over_launches_small_cap(device, monkeypatch, per_head, resid_fmt, cap):
+    """CARRYKERNEL_MAX_ITEMS_PER_LAUNCH lowers what one launch holds, so a
+    small step runs as several launches over slices of the requests (the
+    per-request pointers advanced on the host): bf16 activations and output,
+    strided slot ids, an out-of-place destination, a NULL slot, against the
+    oracle bit for bit, then the same step unsplit for comparison."""
+    B, Hq, HVl, Kl, Vl = 23, 4, 8, 64, 100
+    S = 2 * B + 3
+    rng = np.random.default_rng(cap)
+    pool = make_pool(S, HVl, Vl, Kl, resid_fmt, per_head, seed=cap)
+    perm = (rng.permutation(S - 1) + 1).astype(np.int32)
+    src, dst = perm[:B].copy(), perm[B:2 * B].copy()
+    src[5] = 0
+    mixed, a, b, A_log, dt_bias = make_packed_inputs(B, Hq, HVl, Kl, Vl, seed=cap, dtype=torch.bfloat16)
+    ref_pool = [x.copy() for x in pool]
+    o_ref = oracle.packed_decode(mixed.float().numpy(), a.float().numpy(), b.float().numpy(), A_log.float().numpy(),
+                                 dt_bias.float().numpy(), Kl ** -0.5, *ref_pool, src, Hq, use_qk_l2norm=True,
+                                 resid_fmt=resid_fmt, per_head=per_head, dst_indices=dst)
+    for split in (True, False):
+        if split:
+            monkeypatch.setenv("CARRYKERNEL_MAX_ITEMS_PER_LAUNCH", str(cap))
+        else:
+            monkeypatch.delenv("CARRYKERNEL_MAX_ITEMS_PER_LAUNCH", raising=False)
+        dpool = [torch.from_numpy(x.copy()).to(device) for x in pool]
+        ids2 = torch.zeros(2 * B, dtype=torch.int32)
+        ids2[::2] = torch.from_numpy(src)
+        ids = ids2.to(device)[::2]
+        out = torch.empty(B, 1, HVl, Vl, dtype=torch.bfloat16, device=device)
+        print(f"case split={split} per_head={per_head} cap={cap}", flush=True)
+        qpd.quantized_gated_delta_rule_packed_decode(
+            mixed.to(device), a.to(device), b.to(device), A_log.to(device), dt_bias.to(device), Kl ** -0.5, *dpool,
+            out, ids, use_qk_l2norm_in_kernel=True, resid_fmt=resid_fmt, dst_state_indices=torch.from_numpy(dst).to(device))
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(out[:, 0].float().cpu().numpy(), oracle.bf16_round(o_ref), err_msg=f"out split={split}")
+        for name, d, h in zip(("state_codes", "state_scale", "resid_codes", "resid_scale"), dpool, ref_pool):
+            np.testing.assert_array_equal(_host(d), h, err_msg=f"{name} split={split}")
+
+
+def test_float_state_split_over_launches_small_cap(device, monkeypatch):
+    """The bf16-state arm split into launches of at most 30 items (B=19,
+    HV=8, two 64-row items per head), bit for bit against the oracle."""
+    B, Hq, HVl, Kl, Vl = 19, 8, 8, 128, 128
+    S = B + 2
+    g = torch.Generator().manual_seed(19)
+    state = (torch.randn(S, HVl, Vl, Kl, generator=g) * 0.1).to(torch.bfloat16)
+    ref_state = state.float().numpy().copy()
+    dstate = state.to(device)
+    mixed, a, b, A_log, dt_bias = make_packed_inputs(B, Hq, HVl, Kl, Vl, seed=19)
+    ids = torch.randperm(S - 1, generator=g)[:B].to(torch.int32) + 1
+    out = torch.empty(B, 1, HVl, Vl, device=device)
+    monkeypatch.setenv("CARRYKERNEL_MAX_ITEMS_PER_LAUNCH", "30")
+    print("case float-state split cap=30", flush=True)
+    bench.float_state_step(dstate, mixed.to(device), a.to(device), b.to(device), A_log.to(device),
+                           dt_bias.to(device), Kl ** -0.5, out, ids.to(device), True)
+    torch.cuda.synchronize()
+    o_ref = oracle.packed_decode_float_state(mixed.numpy(), a.numpy(), b.numpy(), A_log.numpy(), dt_bias.numpy(),
+                                             Kl ** -0.5, ref_state, ids.numpy(), Hq, bf16=True, use_qk_l2norm=True)
+    np.testing.assert_array_equal(_host(out[:, 0]), o_ref)
+    np.testing.assert_array_equal(dstate.float().cpu().numpy(), ref_state)
