@@ -413,6 +413,13 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
   const float es_head = R.es_in[0];
 
   float ekeep[PER_HEAD && !EK_LDS ? RPL : 1][16];
+  // Per-row residual scales: lane c of a row group stores row c's output and
+  // both scales after the row loop (every lane of the group holds the reduced
+  // values), so one store instruction covers the group's RPL rows instead of
+  // one 32-byte piece per row (per-row int4, us: B=1 4.76 -> 4.68, B=128
+  // 47.3 -> 46.4; the per-head shape measured level and keeps its stores).
+  constexpr bool MERGED = !PER_HEAD && LPR >= RPL;
+  float o_keep[RPL], s_keep[RPL], es_keep[RPL];
   float4* ek = s_ek + (wave * RPL * 4) * 64 + lane;  // this lane's slots (EK_LDS)
   float eamax_local = 0.0f;
 
@@ -458,7 +465,11 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
     for (int j = 1; j < 16; ++j) o = fmaf(h[j], qq[j], o);
     o = group_sum<LPR>(o);
     asm volatile("" : "+v"(o));  // finish the sum here, where its DPP steps fuse into adds
-    if (c == 0 && valid) store_act_at(obase, (uint32_t)r, odt, o);
+    if constexpr (MERGED) {
+      o_keep[i] = o;
+    } else {
+      if (c == 0 && valid) store_act_at(obase, (uint32_t)r, odt, o);
+    }
 
     // add the carried residual: t = h + e_code * e_scale
     const float es_in = PER_HEAD ? es_head : R.es_in[i];
@@ -500,8 +511,11 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
       } else {
         st_stream16(sbase + (uint32_t)(r * K + c * 16), u32x4{w[0], w[1], w[2], w[3]});
       }
-      if (c == 0) st_at<float>(scb, (uint32_t)r * 4u, s_new);
+      if constexpr (!MERGED) {
+        if (c == 0) st_at<float>(scb, (uint32_t)r * 4u, s_new);
+      }
     }
+    if constexpr (MERGED) s_keep[i] = s_new;
 
     float ea = fabsf(t[0]);
 #pragma unroll
@@ -530,7 +544,29 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
         } else if (lane_in) {
           store_resid<RESID>(ebase + (uint32_t)(r * RKA + c * RKL), eb);
         }
-        if (c == 0) st_at<float>(rsb, (uint32_t)r * 4u, es);
+        if constexpr (!MERGED) {
+          if (c == 0) st_at<float>(rsb, (uint32_t)r * 4u, es);
+        }
+      }
+      if constexpr (MERGED) es_keep[i] = es;
+    }
+  }
+  if constexpr (MERGED) {
+    if (c < RPL) {
+      float ov = o_keep[0], sv = s_keep[0], ev = es_keep[0];
+#pragma unroll
+      for (int j = 1; j < RPL; ++j) {
+        ov = c == j ? o_keep[j] : ov;
+        sv = c == j ? s_keep[j] : sv;
+        ev = c == j ? es_keep[j] : ev;
+      }
+      const int r = row0 + c * L::RPI;
+      if (r < p.V) {
+        store_act_at(obase, (uint32_t)r, odt, ov);
+        if (dst_ok) {
+          st_at<float>(scb, (uint32_t)r * 4u, sv);
+          st_at<float>(rsb, (uint32_t)r * 4u, ev);
+        }
       }
     }
   }
