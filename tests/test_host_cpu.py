@@ -202,6 +202,26 @@ def test_statequant_shape_errors():
                                 z(B, HV, K + 1), z(B, HV, V), z(B, HV), z(B, HV))
 
 
+def test_native_module_host_checks():
+    """cuda/binding.py's contract without a GPU: load_extension raises
+    CudaUnavailable (binding.py:31,49-50); the module's launchers reject a host
+    state with the check_state message (gdn_state_kernel.cu:299-302) before
+    touching the library."""
+    from carrykernel_amd.hip import binding
+    if torch.cuda.is_available():
+        pytest.skip("checks the no-GPU path")
+    with pytest.raises(binding.CudaUnavailable, match="no GPU"):
+        binding.load_extension()
+    with pytest.raises(binding.CudaUnavailable):
+        binding.gdn_fp32_step_cuda(*(torch.zeros(1) for _ in range(6)))
+    ext = binding.HipModule(None)
+    z = torch.zeros
+    with pytest.raises(RuntimeError, match="h_in must be a CUDA tensor"):
+        ext.gdn_quant_step(z(1, 1, 4, 4, dtype=torch.int8), *(z(1) for _ in range(13)), 127.0, 0, 128)
+    with pytest.raises(RuntimeError, match="h_in must be a CUDA tensor"):
+        ext.gdn_fp32_step(z(1, 1, 4, 4), *(z(1) for _ in range(7)), 128)
+
+
 def test_debug_index_checks():
     qpd._check_indices_host(torch.tensor([0, 2, 3, 0], dtype=torch.int32), 4)
     with pytest.raises(ValueError, match="duplicate"):

@@ -278,3 +278,41 @@ def test_per_v_channel_quantize_shapes_and_ties(device, K, V):
     np.testing.assert_array_equal(scale.cpu().numpy(), s_ref)
     assert torch.all(scale.cpu()[:, 0] == 1.0)
     assert codes.cpu()[0, :len(ties), 0].tolist() == [2, -4, 0, 0, 2, 126]
+
+
+@pytest.mark.parametrize("res_fmt", [sq.RES_FP32, sq.RES_INT8])
+def test_native_module_boundary(device, res_fmt):
+    """The extension module's launchers (cuda/gdn_state_kernel.cu:310-371) as
+    binding.load_extension() exposes them: outputs owned by the caller, bytes
+    equal to the wrapper's, TORCH_CHECK failures as RuntimeError."""
+    B, HV, K, V = 2, 4, 32, 64
+    codes, scale, e, es = _random_state(B, HV, K, V, res_fmt, seed=21)
+    _, q, k, v, alpha, beta = make_inputs(1, B, HV, K, V, seed=22)
+    d = [t.to(device) if t is not None else None for t in (codes, scale, e, es, q[0], k[0], v[0], alpha[0], beta[0])]
+    want = binding.gdn_quant_step_hip(*d, 8, res_fmt)
+    ext = binding.load_extension()
+    es_in = d[3] if d[3] is not None else torch.zeros(B, HV, V, device=device)
+    outs = (torch.empty(B, HV, V, device=device), torch.empty(B, HV, K, V, dtype=torch.int8, device=device),
+            torch.empty(B, HV, V, device=device), torch.empty_like(d[2]), torch.empty(B, HV, V, device=device))
+    ext.gdn_quant_step(d[0], d[1], d[2], es_in, *d[4:], *outs, 127.0, res_fmt, 128)
+    torch.cuda.synchronize()
+    for got, ref in zip(outs, want):
+        if ref is not None:
+            assert torch.equal(got.view(torch.uint8) if got.dtype == torch.int8 else got,
+                               ref.view(torch.uint8) if ref.dtype == torch.int8 else ref)
+    with pytest.raises(RuntimeError, match="block_v must be in"):
+        ext.gdn_quant_step(d[0], d[1], d[2], es_in, *d[4:], *outs, 127.0, res_fmt, 0)
+    with pytest.raises(RuntimeError, match="h_in must be int8"):
+        ext.gdn_quant_step(d[1], d[1], d[2], es_in, *d[4:], *outs, 127.0, res_fmt, 128)
+    with pytest.raises(RuntimeError, match="q must be"):
+        ext.gdn_quant_step(d[0], d[1], d[2], es_in, d[4][:1], *d[5:], *outs, 127.0, res_fmt, 128)
+    with pytest.raises(RuntimeError, match="unknown res_fmt"):
+        ext.gdn_quant_step(d[0], d[1], d[2], es_in, *d[4:], *outs, 127.0, 9, 128)
+    h32 = torch.randn(B, HV, K, V, device=device)
+    o, h_out = torch.empty(B, HV, V, device=device), torch.empty_like(h32)
+    ext.gdn_fp32_step(h32, *d[4:], o, h_out, 128)
+    ref_h, ref_o = binding.gdn_fp32_step_hip(h32, *d[4:])
+    torch.cuda.synchronize()
+    assert torch.equal(h_out, ref_h) and torch.equal(o, ref_o)
+    with pytest.raises(RuntimeError, match="h_in must be fp32"):
+        ext.gdn_fp32_step(d[0], *d[4:], o, h_out, 128)
