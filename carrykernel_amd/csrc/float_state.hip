@@ -8,8 +8,9 @@
 // lane map (a lane owns 16 consecutive K of a V-row: 64 bytes of fp32 or 32 of
 // bf16), persistent workgroups of 4 waves x 2 rows per lane (64-row tiles)
 // looping over items with the next item's state rows, v and q/k prefetched
-// into a second register set, q/k staged once per item in LDS, gates of 64
-// items evaluated lane-parallel, DPP row reductions. Per row:
+// into a second register set, q/k staged once per item in LDS, the gates of
+// all of a workgroup's items evaluated lane-parallel into LDS before the item
+// loop, DPP row reductions. Per row:
 //   h_j = h_j * alpha;  rd = sum_j h_j k_j;  dv = beta * (v - rd)
 //   h_j = fma(k_j, dv, h_j);  o = sum_j h_j q_j;  state <- h (bf16: RNE)
 #include <hip/hip_runtime.h>

@@ -22,7 +22,7 @@
 // carry raw bits (activation conversion happens at use), so issuing them never
 // waits. q and k are staged once per item through LDS (double-buffered, one
 // barrier per item). The gates of all of a workgroup's items are evaluated
-// together, one item per lane, and read back with v_readlane.
+// before its item loop, one item per lane, into an LDS table (stage_gates).
 //
 // Arithmetic per row (FAST mode; EXACT differs where ck_quant.h says):
 //   sa = s_in * alpha;  h_j = code_j * sa
