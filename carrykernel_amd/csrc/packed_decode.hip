@@ -10,13 +10,13 @@
 namespace ck {
 namespace pd {
 
-int launch_masked(const PackedParams& p, int B, int resid_fmt, int per_head, int mode, bool lanes,
+int launch_masked(const PackedParams& p, int B, int resid_fmt, int per_head, int mode, int access,
                   hipStream_t stream) {
-  if (p.K <= 16) return launch_masked_k<16>(p, B, resid_fmt, per_head, mode, lanes, stream);
-  if (p.K <= 32) return launch_masked_k<32>(p, B, resid_fmt, per_head, mode, lanes, stream);
-  if (p.K <= 64) return launch_masked_k<64>(p, B, resid_fmt, per_head, mode, lanes, stream);
-  if (p.K <= 128) return launch_masked_k<128>(p, B, resid_fmt, per_head, mode, lanes, stream);
-  return launch_masked_k<256>(p, B, resid_fmt, per_head, mode, lanes, stream);
+  if (p.K <= 16) return launch_masked_k<16>(p, B, resid_fmt, per_head, mode, access, stream);
+  if (p.K <= 32) return launch_masked_k<32>(p, B, resid_fmt, per_head, mode, access, stream);
+  if (p.K <= 64) return launch_masked_k<64>(p, B, resid_fmt, per_head, mode, access, stream);
+  if (p.K <= 128) return launch_masked_k<128>(p, B, resid_fmt, per_head, mode, access, stream);
+  return launch_masked_k<256>(p, B, resid_fmt, per_head, mode, access, stream);
 }
 
 int resident_workgroups(const void* fn, int block, int* per_cu_out) {
@@ -156,7 +156,15 @@ static int packed_decode_impl(const void* mixed_qkv, int qkv_dtype, int64_t stri
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int per_head = rscale_mode == CK_RSCALE_PER_HEAD;
   const int mode = quant_mode == CK_QUANT_EXACT ? kExact : kFast;
-  if (!pow2_k || !rows_aligned) return launch_masked(p, B, resid_fmt, per_head, mode, rows_aligned && K % 16 == 0, s);
+  if (!pow2_k || !rows_aligned) {
+    // 4-byte state rows (and int8 residual rows; int4 residual rows of K / 2
+    // bytes are then 2-byte aligned) take word accesses
+    const int walign = resid_fmt == CK_RESID_INT4 ? 2 : 4;
+    const bool words = K % 4 == 0 && !(reinterpret_cast<uintptr_t>(state_codes) & 3) && stride_state_slot % 4 == 0 &&
+                       !(reinterpret_cast<uintptr_t>(resid_codes) & (walign - 1)) && stride_resid_slot % walign == 0;
+    const int access = rows_aligned && K % 16 == 0 ? kMaskLanes : words ? kMaskWords : kMaskBytes;
+    return launch_masked(p, B, resid_fmt, per_head, mode, access, s);
+  }
   switch (K) {
     case 16: return launch_for_k<16>(p, B, resid_fmt, per_head, mode, qkv_dtype, s);
     case 32: return launch_for_k<32>(p, B, resid_fmt, per_head, mode, qkv_dtype, s);

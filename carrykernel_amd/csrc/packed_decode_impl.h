@@ -357,10 +357,41 @@ __device__ __forceinline__ void store_resid_masked(int8_t* dst, const uint32_t (
 // value past p.K). kMaskBytes: any p.K and alignment, byte by byte.
 // kMaskLanes: p.K a multiple of 16 with aligned rows, so a lane's 16 codes
 // (and 8 or 16 residual bytes) are all there or all past p.K, and it loads and
-// stores them whole.
+// stores them whole. kMaskWords: p.K a multiple of 4 with 4-byte-aligned state
+// rows (and int8 residual rows; an int4 residual row of p.K / 2 bytes is then
+// 2-byte aligned): 4-byte state and int8-residual accesses, 2-byte int4
+// residual ones, each all there or all past p.K.
 constexpr int kMaskNone = 0;
 constexpr int kMaskBytes = 1;
 constexpr int kMaskLanes = 2;
+constexpr int kMaskWords = 3;
+
+// The first n bytes (n a multiple of 4, clamped to 0 .. 4 NW) of w, one
+// 4-byte store per word.
+template <int NW>
+__device__ __forceinline__ void st_words_masked(int8_t* dst, const uint32_t (&w)[NW], int n) {
+#pragma unroll
+  for (int j = 0; j < NW; ++j)
+    if (4 * j < n) *reinterpret_cast<uint32_t*>(dst + 4 * j) = w[j];
+}
+
+// A lane's residual bytes under kMaskWords: int8 in 4-byte words, int4 (n
+// even) in 2-byte halves.
+template <int RESID>
+__device__ __forceinline__ void store_resid_words(int8_t* dst, const uint32_t (&eb)[16], int n) {
+  if constexpr (RESID == kResidInt4) {
+    const uint32_t w0[8] = {eb[0], eb[1], eb[2], eb[3], eb[4], eb[5], eb[6], eb[7]};
+    const uint32_t w1[8] = {eb[8], eb[9], eb[10], eb[11], eb[12], eb[13], eb[14], eb[15]};
+    const uint32_t w[2] = {pack_nibbles8(w0), pack_nibbles8(w1)};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (2 * j < n) *reinterpret_cast<uint16_t*>(dst + 2 * j) = (uint16_t)(w[j >> 1] >> (16 * (j & 1)));
+  } else {
+    const uint32_t w[4] = {pack_low_bytes(eb[0], eb[1], eb[2], eb[3]), pack_low_bytes(eb[4], eb[5], eb[6], eb[7]),
+                           pack_low_bytes(eb[8], eb[9], eb[10], eb[11]), pack_low_bytes(eb[12], eb[13], eb[14], eb[15])};
+    st_words_masked<4>(dst, w, n);
+  }
+}
 
 // Compute and store one item whose registers are loaded (MASK: see above).
 template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ACT, bool DST, int MASK = kMaskNone>
@@ -506,6 +537,8 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
                              pack_low_bytes(yb[8], yb[9], yb[10], yb[11]), pack_low_bytes(yb[12], yb[13], yb[14], yb[15])};
       if constexpr (MASK == kMaskBytes) {
         st_bytes_masked<4>(sbase + (uint32_t)(r * KA + c * 16), w, KA - c * 16);
+      } else if constexpr (MASK == kMaskWords) {
+        st_words_masked<4>(sbase + (uint32_t)(r * KA + c * 16), w, KA - c * 16);
       } else if constexpr (MASK == kMaskLanes) {
         if (lane_in) st_stream16(sbase + (uint32_t)(r * KA + c * 16), u32x4{w[0], w[1], w[2], w[3]});
       } else {
@@ -541,6 +574,8 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
       if (store) {
         if constexpr (MASK == kMaskBytes) {
           store_resid_masked<RESID>(ebase + (uint32_t)(r * RKA + c * RKL), eb, RKA - c * RKL);
+        } else if constexpr (MASK == kMaskWords) {
+          store_resid_words<RESID>(ebase + (uint32_t)(r * RKA + c * RKL), eb, RKA - c * RKL);
         } else if (lane_in) {
           store_resid<RESID>(ebase + (uint32_t)(r * RKA + c * RKL), eb);
         }
@@ -599,6 +634,8 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
       if (r < p.V && dst_ok) {
         if constexpr (MASK == kMaskBytes) {
           store_resid_masked<RESID>(ebase + (uint32_t)(r * RKA + c * RKL), eb, RKA - c * RKL);
+        } else if constexpr (MASK == kMaskWords) {
+          store_resid_words<RESID>(ebase + (uint32_t)(r * RKA + c * RKL), eb, RKA - c * RKL);
         } else if (lane_in) {
           store_resid<RESID>(ebase + (uint32_t)(r * RKA + c * RKL), eb);
         }
@@ -1026,9 +1063,9 @@ int launch_for_k(const PackedParams& p, int B, int resid_fmt, int per_head, int 
 
 // Any K in 1 .. 256 and any row alignment (packed_decode_masked.h): the lane
 // map of K rounded up to a power of two (at least 16), values past p.K zero,
-// one item per workgroup; lanes: whole-lane accesses (p.K a multiple of 16,
-// aligned rows), else byte-granular ones.
-int launch_masked(const PackedParams& p, int B, int resid_fmt, int per_head, int mode, bool lanes,
+// one item per workgroup; access: kMaskLanes (p.K a multiple of 16, aligned
+// rows), kMaskWords (p.K a multiple of 4, 4-byte-aligned rows) or kMaskBytes.
+int launch_masked(const PackedParams& p, int B, int resid_fmt, int per_head, int mode, int access,
                   hipStream_t stream);
 
 #define CK_PD_DEFINE_LAUNCH_FOR_K(KV)                                                                     \

@@ -54,6 +54,20 @@ __device__ __forceinline__ void load_item_masked(const PackedParams& p, const It
           e[0] = e4.x, e[1] = e4.y, e[2] = e4.z, e[3] = e4.w;
         }
       }
+    } else if constexpr (MASK == kMaskWords) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (c * 16 + 4 * j < K) w[j] = *reinterpret_cast<const uint32_t*>(srow + c * 16 + 4 * j);
+      if constexpr (RESID == kResidInt4) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (c * RKL + 2 * j < RKA)
+            e[j >> 1] |= (uint32_t)*reinterpret_cast<const uint16_t*>(erow + c * RKL + 2 * j) << (16 * (j & 1));
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (c * RKL + 4 * j < RKA) e[j] = *reinterpret_cast<const uint32_t*>(erow + c * RKL + 4 * j);
+      }
     } else {
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
@@ -147,7 +161,7 @@ template <int KP, int RESID, bool PER_HEAD, int MODE, bool DST, int MASK>
 int launch_masked_shape(const PackedParams& p, int B, hipStream_t s) {
   constexpr int RPI = 64 / (KP / 16);
   if constexpr (!PER_HEAD) {
-    if constexpr (MASK == kMaskBytes) {
+    if constexpr (MASK == kMaskBytes || MASK == kMaskWords) {
       return launch_masked_cfg<KP, 1, 4, RESID, false, MODE, DST, MASK>(p, B, s);
     } else {
       const int64_t tiles = (int64_t)B * p.HV * ((p.V + RPI * 4 - 1) / (RPI * 4));
@@ -186,20 +200,22 @@ int launch_masked_mode(const PackedParams& p, int B, int resid_fmt, int per_head
                         : launch_masked_shape<KP, kResidInt8, false, kExact, false, MASK>(p, B, s));
 }
 
-// lanes: p.K is a multiple of 16 and the rows are aligned for whole-lane
-// accesses (only below a power-of-two KP >= 64: K = 16 and 32 are powers of
-// two, which the bandwidth kernel takes when aligned).
+// access: kMaskLanes when p.K is a multiple of 16 and the rows are aligned for
+// whole-lane accesses (only below a power-of-two KP >= 64: K = 16 and 32 are
+// powers of two, which the bandwidth kernel takes when aligned), kMaskWords
+// when p.K is a multiple of 4 with 4-byte-aligned rows, else kMaskBytes.
 template <int KP>
-int launch_masked_k(const PackedParams& p, int B, int resid_fmt, int per_head, int mode, bool lanes, hipStream_t s);
+int launch_masked_k(const PackedParams& p, int B, int resid_fmt, int per_head, int mode, int access, hipStream_t s);
 
 #define CK_PD_DEFINE_MASKED_FOR_K(KP)                                                                        \
   template <>                                                                                                \
-  int launch_masked_k<KP>(const PackedParams& p, int B, int resid_fmt, int per_head, int mode, bool lanes,  \
+  int launch_masked_k<KP>(const PackedParams& p, int B, int resid_fmt, int per_head, int mode, int access,   \
                           hipStream_t s) {                                                                   \
     if constexpr (KP >= 64) {                                                                                \
-      if (lanes) return launch_masked_mode<KP, kMaskLanes>(p, B, resid_fmt, per_head, mode, s);              \
+      if (access == kMaskLanes) return launch_masked_mode<KP, kMaskLanes>(p, B, resid_fmt, per_head, mode, s); \
     }                                                                                                        \
-    (void)lanes;                                                                                             \
+    if (access == kMaskWords || access == kMaskLanes)                                                        \
+      return launch_masked_mode<KP, kMaskWords>(p, B, resid_fmt, per_head, mode, s);                         \
     return launch_masked_mode<KP, kMaskBytes>(p, B, resid_fmt, per_head, mode, s);                           \
   }
 

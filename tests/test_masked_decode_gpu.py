@@ -1,6 +1,7 @@
 """GPU parity of the any-K decode path (packed_decode_masked.h): pool rows
 whose K is not a power of two from 16 (K = 2 ... 240: byte-granular
-accesses, or whole 16-byte lanes when K is a multiple of 16), and
+accesses, 4-byte state and 2- or 4-byte residual accesses when K is a
+multiple of 4, or whole 16-byte lanes when K is a multiple of 16), and
 power-of-two K whose pool rows are not aligned for the bandwidth kernel's
 16-byte lane loads (byte-granular). The reference computes such rows as if
 zero-padded to its power-of-two lane count (quantized_packed_decode.py:
@@ -49,6 +50,9 @@ CASES = {
     "k96_int4_row_lanes_many_tiles": (96, 64, 2, 8, 128, I4, False, "fast", F32, F32, True, 0.1, True, False, 8, 2,
                                       False),
     "k240_int8_head_lanes": (240, 3, 1, 3, 100, I8, True, "fast", F32, F32, False, 0.0, False, False, 6, 2, False),
+    # K a multiple of 4: word accesses; int4 residual rows of K / 2 = 50 and 10 bytes are 2-byte aligned
+    "k100_int4_row_words": (100, 6, 2, 4, 64, I4, False, "fast", F32, F32, True, 0.0, False, False, 8, 2, False),
+    "k20_int4_head_words_exact": (20, 4, 1, 2, 40, I4, True, "exact", F32, F32, True, 0.1, True, False, 8, 2, False),
     "k128_misaligned_int4_head": (128, 8, 4, 8, 128, I4, True, "fast", F32, F32, True, 0.1, True, False, 8, 2,
                                   True),
     "k64_misaligned_int8_row_exact": (64, 8, 2, 4, 100, I8, False, "exact", BF16, F32, False, 0.0, False, False, 8,
