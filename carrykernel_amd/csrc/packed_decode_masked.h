@@ -150,13 +150,14 @@ int launch_masked_cfg(PackedParams p, int B, hipStream_t stream) {
 }
 
 // Shapes: per-row residual scales take tiles of RPI * 4 rows, as 4 waves of
-// one row per lane with byte accesses (more loads in flight) or with fewer
-// than 2048 tiles (a small batch's rows over more SIMDs), else one wave of 4
-// rows per lane (per-workgroup set-up spread over more rows): K=100 bytes,
-// B=1 / 8 / 64 at HV=32: 18.5 / 23.4 / 112 -> 8.2 / 17.0 / 105 us; K=96
-// lanes: B=1 / 8 6.8 / 7.7 -> 4.5 / 6.7 us, B=64 24.3 us kept (31.6 with one
-// row per lane). A per-head scale needs the whole head in one workgroup, the
-// fewest waves of 4 rows per lane that cover V.
+// one row per lane with byte or word accesses (more loads in flight) or with
+// fewer than 2048 tiles (a small batch's rows over more SIMDs), else one wave
+// of 4 rows per lane (per-workgroup set-up spread over more rows): K=100
+// bytes, B=1 / 8 / 64 at HV=32: 18.5 / 23.4 / 112 -> 8.2 / 17.0 / 105 us;
+// K=100 words, B=64: 32.7 us (37.1 with 4 rows per lane); K=96 lanes: B=1 / 8
+// 6.8 / 7.7 -> 4.5 / 6.7 us, B=64 24.3 us kept (31.6 with one row per lane).
+// A per-head scale needs the whole head in one workgroup, the fewest waves of
+// 4 rows per lane that cover V.
 template <int KP, int RESID, bool PER_HEAD, int MODE, bool DST, int MASK>
 int launch_masked_shape(const PackedParams& p, int B, hipStream_t s) {
   constexpr int RPI = 64 / (KP / 16);
