@@ -156,8 +156,11 @@ int launch_masked_cfg(PackedParams p, int B, hipStream_t stream) {
 // bytes, B=1 / 8 / 64 at HV=32: 18.5 / 23.4 / 112 -> 8.2 / 17.0 / 105 us;
 // K=100 words, B=64: 32.7 us (37.1 with 4 rows per lane); K=96 lanes: B=1 / 8
 // 6.8 / 7.7 -> 4.5 / 6.7 us, B=64 24.3 us kept (31.6 with one row per lane).
-// A per-head scale needs the whole head in one workgroup, the fewest waves of
-// 4 rows per lane that cover V.
+// A per-head scale needs the whole head in one workgroup: at KP=128 a head of
+// 65 to 128 rows takes 8 waves of 2 rows per lane (two workgroups per CU, as
+// the bandwidth kernel's shape; B=64, HV=32, V=128: K=100 int4 words 40.9 ->
+// 34.3 us, K=128 one byte off alignment 121.0 -> 105.7 us against 4 waves of 4
+// rows), otherwise the fewest waves of 4 rows per lane that cover V.
 template <int KP, int RESID, bool PER_HEAD, int MODE, bool DST, int MASK>
 int launch_masked_shape(const PackedParams& p, int B, hipStream_t s) {
   constexpr int RPI = 64 / (KP / 16);
@@ -170,6 +173,9 @@ int launch_masked_shape(const PackedParams& p, int B, hipStream_t s) {
       return launch_masked_cfg<KP, 4, 1, RESID, false, MODE, DST, MASK>(p, B, s);
     }
   } else {
+    if constexpr (KP == 128) {
+      if (p.V > RPI * 4 * 2 && p.V <= RPI * 2 * 8) return launch_masked_cfg<KP, 2, 8, RESID, true, MODE, DST, MASK>(p, B, s);
+    }
     if (p.V <= RPI * 4 * 1) return launch_masked_cfg<KP, 4, 1, RESID, true, MODE, DST, MASK>(p, B, s);
     if (p.V <= RPI * 4 * 2) return launch_masked_cfg<KP, 4, 2, RESID, true, MODE, DST, MASK>(p, B, s);
     if (p.V <= RPI * 4 * 4) return launch_masked_cfg<KP, 4, 4, RESID, true, MODE, DST, MASK>(p, B, s);

@@ -52,6 +52,7 @@ CASES = {
     "k240_int8_head_lanes": (240, 3, 1, 3, 100, I8, True, "fast", F32, F32, False, 0.0, False, False, 6, 2, False),
     # K a multiple of 4: word accesses; int4 residual rows of K / 2 = 50 and 10 bytes are 2-byte aligned
     "k100_int4_row_words": (100, 6, 2, 4, 64, I4, False, "fast", F32, F32, True, 0.0, False, False, 8, 2, False),
+    "k100_int4_head_words_gqa": (100, 4, 2, 8, 120, I4, True, "fast", BF16, F32, True, 0.2, True, False, 8, 2, False),
     "k20_int4_head_words_exact": (20, 4, 1, 2, 40, I4, True, "exact", F32, F32, True, 0.1, True, False, 8, 2, False),
     "k128_misaligned_int4_head": (128, 8, 4, 8, 128, I4, True, "fast", F32, F32, True, 0.1, True, False, 8, 2,
                                   True),
