@@ -160,7 +160,9 @@ int launch_masked_cfg(PackedParams p, int B, hipStream_t stream) {
 // 65 to 128 rows takes 8 waves of 2 rows per lane (two workgroups per CU, as
 // the bandwidth kernel's shape; B=64, HV=32, V=128: K=100 int4 words 40.9 ->
 // 34.3 us, K=128 one byte off alignment 121.0 -> 105.7 us against 4 waves of 4
-// rows), otherwise the fewest waves of 4 rows per lane that cover V.
+// rows), at KP=256 a head of 65 to 128 rows 16 waves of 2 rows per lane (K=200
+// int4 100.7 -> 87.2 us, K=256 misaligned 232.5 -> 209.2 us against 8 waves of
+// 4 rows), otherwise the fewest waves of 4 rows per lane that cover V.
 template <int KP, int RESID, bool PER_HEAD, int MODE, bool DST, int MASK>
 int launch_masked_shape(const PackedParams& p, int B, hipStream_t s) {
   constexpr int RPI = 64 / (KP / 16);
@@ -175,6 +177,10 @@ int launch_masked_shape(const PackedParams& p, int B, hipStream_t s) {
   } else {
     if constexpr (KP == 128) {
       if (p.V > RPI * 4 * 2 && p.V <= RPI * 2 * 8) return launch_masked_cfg<KP, 2, 8, RESID, true, MODE, DST, MASK>(p, B, s);
+    }
+    if constexpr (KP == 256) {
+      if (p.V > RPI * 4 * 4 && p.V <= RPI * 2 * 16)
+        return launch_masked_cfg<KP, 2, 16, RESID, true, MODE, DST, MASK>(p, B, s);
     }
     if (p.V <= RPI * 4 * 1) return launch_masked_cfg<KP, 4, 1, RESID, true, MODE, DST, MASK>(p, B, s);
     if (p.V <= RPI * 4 * 2) return launch_masked_cfg<KP, 4, 2, RESID, true, MODE, DST, MASK>(p, B, s);
