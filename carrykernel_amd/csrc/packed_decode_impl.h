@@ -1013,6 +1013,15 @@ int launch_k(const PackedParams& p, int B, hipStream_t stream) {
     if constexpr (K == 128) {
       if (need > RPI * 4 * 2 && need <= RPI * 2 * 8) return launch_cfg<K, 2, 8, RESID, true, MODE, ACT, DST>(p, B, stream);
     }
+    // K=256: 8 waves of 4 rows per lane take 230 VGPRs, one 8-wave workgroup
+    // per CU; from one head per CU on, 16 waves of 2 rows (128 VGPRs, four
+    // waves per SIMD) hide more latency (int4 per head, H=HV=32, graph-
+    // replayed, us: B=8 10.3 -> 9.8, B=16 16.8 -> 16.0, B=64 51.1 -> 49.5);
+    // fewer heads stay on the 8-wave shape (B=1 9.1 against 9.7)
+    if constexpr (K == 256) {
+      if (need > RPI * 4 * 4 && need <= RPI * 2 * 16 && (int64_t)B * p.HV >= 256)
+        return launch_cfg<K, 2, 16, RESID, true, MODE, ACT, DST>(p, B, stream);
+    }
     // fewer rows per lane over more waves for a V=128 head at small K (per-head,
     // int4, HV=32, us at B=1 / 64): K=64 2 rows x 4 waves 6.9 / 16.1 -> 5.7 /
     // 14.8; K=16 1 row x 2 waves 6.2 / 9.2 -> 4.9 / 8.7; K=32 1 row x 4 waves

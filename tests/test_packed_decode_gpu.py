@@ -92,6 +92,15 @@ def test_bit_exact_small_k_per_head_shapes(device, K, B, HV, resid_fmt, mode):
               mode=mode, l2norm=True, T=2, seed=K + B)
 
 
+@pytest.mark.parametrize("resid_fmt", [qpd.RESID_INT8, qpd.RESID_INT4])
+@pytest.mark.parametrize("mode", ["fast", "exact"])
+def test_bit_exact_k256_per_head_16_waves(device, resid_fmt, mode):
+    """A V=128 head at K=256 with a per-head residual scale from one head per
+    CU on (B x HV >= 256): 16 waves of 2 rows per lane."""
+    _run_both(device, B=8, H=16, HV=32, K=256, V=128, resid_fmt=resid_fmt, per_head=True,
+              mode=mode, l2norm=True, T=2, seed=256)
+
+
 @pytest.mark.parametrize("act_dtype,out_dtype", [(torch.bfloat16, torch.bfloat16),
                                                  (torch.float16, torch.float32),
                                                  (torch.float32, torch.bfloat16)])
