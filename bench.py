@@ -1004,11 +1004,11 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8 state / int4 residual, fp32 arithmetic",
+        "dtype": "f32",   # the arithmetic; storage: int8 state codes, int4 / int8 residual codes (config)
         "data": "synthetic (config distributions; state from 64 fp32 warm-up steps)",
         "config": {"workload": "C3: single-layer fused decode, int8 per-V state + packed int4 EF residual "
                                "(per-head scale), vLLM [slots,HV,V,K] layout",
-                   "batch": B, "value_heads": HV, "qk_heads": H, "K": K, "V": V,
+                   "batch": B, "value_heads": HV, "qk_heads": H, "K": K, "V": V, "state": "int8",
                    "resid": args.resid, "resid_scale": args.rscale, "quant_mode": args.quant_mode,
                    "pool_slots": B * args.groups + 1},
         "validated": r["validated"],
