@@ -1018,7 +1018,9 @@ def main():
         "bytes_vs_bf16_state": round(bf16_state_bytes(B, H, HV, K, V) / nbytes, 4),
     }
     traffic_path = os.path.join(HERE, "profiles", "traffic_packed_decode_b64.json")
-    if os.path.exists(traffic_path):
+    # the measured traffic belongs to the headline configuration only
+    headline = (B == 64 and args.resid == "int4" and args.rscale == "head" and args.quant_mode == "fast")
+    if headline and os.path.exists(traffic_path):
         with open(traffic_path) as f:
             line["roofline"]["traffic"] = json.load(f).get("traffic_bytes_per_launch")
     # batch sweep of the same format (config C3) in both arithmetic modes at
