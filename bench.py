@@ -26,6 +26,7 @@ launch stream.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -340,35 +341,68 @@ def _capture(device, step, ts):
     return graph
 
 
+_hip_runtime = None
+
+
+def _graph_upload(graph, device):
+    """hipGraphUpload of an instantiated graph on the launch stream: puts the
+    graph's launch packets and kernel arguments on the device without running
+    it, so its first replay costs what every later one does."""
+    global _hip_runtime
+    if _hip_runtime is None:
+        # the HIP runtime torch itself loaded (same file, so the same handle)
+        hip = ctypes.CDLL(os.path.join(os.path.dirname(torch.__file__), "lib", "libamdhip64.so"))
+        hip.hipGraphUpload.restype = ctypes.c_int
+        hip.hipGraphUpload.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        _hip_runtime = hip
+    st = _hip_runtime.hipGraphUpload(graph.raw_cuda_graph_exec(),
+                                     torch.cuda.current_stream(device).cuda_stream)
+    if st != 0:
+        raise RuntimeError(f"hipGraphUpload failed with status {st}")
+    return graph
+
+
 class StepReplayer:
-    """Replays exactly n launches of step(t): n // period replays of a graph
-    of steps 0 .. period-1, then one graph of the first n % period steps."""
+    """Exactly `warmup` untimed launches of step(t), then exactly `steps`
+    timed ones, all graph-replayed. Every graph is captured and uploaded when
+    the replayer is built, so nothing is captured between the warm-up and the
+    timed region and no graph's first replay is timed. The warm-up is
+    warmup // period replays of a graph of steps 0 .. period-1 plus one graph
+    of the remainder; the timed steps are replays of one graph of
+    min(steps, MAX_GRAPH_STEPS) steps plus one graph of the remainder, so a
+    short run is one or two graph launches."""
 
-    def __init__(self, device, step, period):
-        self.device, self.step, self.period = device, step, period
-        self.full = _capture(device, step, range(period))
-        self.tails = {}
+    MAX_GRAPH_STEPS = 1024
 
-    def replay(self, n):
-        for _ in range(n // self.period):
-            self.full.replay()
-        r = n % self.period
-        if r:
-            if r not in self.tails:
-                self.tails[r] = _capture(self.device, self.step, range(r))
-            self.tails[r].replay()
+    def __init__(self, device, step, period, steps, warmup):
+        self.device, self.steps, self.warmup = device, steps, warmup
 
-    def time_ms_per_step(self, steps, warmup):
-        """Exactly `warmup` untimed steps, then exactly `steps` steps between
-        two HIP events on the launch stream, synchronised on both sides."""
-        if steps % self.period:
-            self.replay(steps % self.period)   # capture the remainder graph outside the timed region
-        self.replay(warmup)
+        def graph(n):
+            return _graph_upload(_capture(device, step, range(n)), device) if n > 0 else None
+
+        self.warm_full = graph(period) if warmup >= period else None
+        self.warm_reps = warmup // period
+        self.warm_tail = graph(warmup % period)
+        n_big = min(steps, self.MAX_GRAPH_STEPS)
+        self.big = graph(n_big)
+        self.big_reps = steps // n_big if n_big > 0 else 0
+        self.tail = graph(steps - self.big_reps * n_big)
+
+    def time_ms_per_step(self):
+        """The warm-up, a synchronize, then the timed steps between two HIP
+        events on the launch stream, and a synchronize."""
+        for _ in range(self.warm_reps):
+            self.warm_full.replay()
+        if self.warm_tail is not None:
+            self.warm_tail.replay()
         torch.cuda.synchronize()
         timer = Timer(self.device)
         timer.start()
-        self.replay(steps)
-        ms = timer.stop_ms() / steps
+        for _ in range(self.big_reps):
+            self.big.replay()
+        if self.tail is not None:
+            self.tail.replay()
+        ms = timer.stop_ms() / self.steps
         torch.cuda.synchronize()
         return ms
 
@@ -417,8 +451,10 @@ def run_config(device, B, resid_fmt, per_head, steps, warmup, groups, quant_mode
     torch.cuda.synchronize()
     host_ms = (time.perf_counter() - t0) * 1e3 / n_eager
 
-    rep = StepReplayer(device, step, groups)
-    ms = rep.time_ms_per_step(steps, warmup)
+    # captured after the eager calls: a short timed run straight after them
+    # (graphs captured first) runs up to 15 % slower per step at B=256
+    rep = StepReplayer(device, step, groups, steps, warmup)
+    ms = rep.time_ms_per_step()
     if not torch.isfinite(out.float()).all():
         raise RuntimeError("non-finite output in the timed run")
     del rep, pool
