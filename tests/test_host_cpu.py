@@ -297,6 +297,49 @@ def test_bench_refuses_more_than_one_gpu():
     assert "only --gpus 1" in r.stderr and r.stdout == ""
 
 
+@pytest.mark.parametrize("steps,warmup,period", [(20, 5, 16), (2000, 200, 16), (1, 0, 16), (1024, 16, 16),
+                                                 (1025, 17, 16), (3000, 3, 8), (16, 15, 16)])
+def test_bench_times_exactly_k_steps(monkeypatch, steps, warmup, period):
+    """The bench's replayer runs exactly `warmup` steps before the start
+    event, exactly `steps` steps between the two events and nothing after; the
+    timed steps are at most ceil(steps / 1024) + 1 graph launches, and every
+    graph is captured (and uploaded) before the warm-up."""
+    import bench
+    log, marks = [], {}
+
+    class FakeGraph:
+        def __init__(self, n):
+            self.n = n
+            marks.setdefault("captures_at", []).append(len(log))
+
+        def replay(self):
+            log.append(self.n)
+
+    class FakeTimer:
+        def __init__(self, device):
+            pass
+
+        def start(self):
+            marks["start"] = len(log)
+
+        def stop_ms(self):
+            marks["stop"] = len(log)
+            return 1.0
+
+    monkeypatch.setattr(bench, "_capture", lambda device, step, ts: FakeGraph(len(ts)))
+    monkeypatch.setattr(bench, "_graph_upload", lambda graph, device: graph)
+    monkeypatch.setattr(bench, "Timer", FakeTimer)
+    monkeypatch.setattr(bench.torch.cuda, "synchronize", lambda *a, **k: None)
+    rep = bench.StepReplayer("cpu", None, period, steps, warmup)
+    ms = rep.time_ms_per_step()
+    assert all(at == 0 for at in marks["captures_at"])
+    assert sum(log[:marks["start"]]) == warmup
+    assert sum(log[marks["start"]:marks["stop"]]) == steps
+    assert len(log) == marks["stop"]
+    assert marks["stop"] - marks["start"] <= -(-steps // bench.StepReplayer.MAX_GRAPH_STEPS) + 1
+    assert ms == pytest.approx(1.0 / steps)
+
+
 def test_init_quantized_state_checks_h0_before_allocating():
     """init_quantized_state rejects an h0 of the wrong shape or a non-float
     dtype with ValueError before it touches a device; a float h0 on the host
