@@ -350,8 +350,13 @@ def _graph_upload(graph, device):
     it, so its first replay costs what every later one does."""
     global _hip_runtime
     if _hip_runtime is None:
-        # the HIP runtime torch itself loaded (same file, so the same handle)
-        hip = ctypes.CDLL(os.path.join(os.path.dirname(torch.__file__), "lib", "libamdhip64.so"))
+        # the HIP runtime already mapped into this process (the one torch
+        # uses): opening that same file returns the loaded library's handle
+        with open("/proc/self/maps") as maps:
+            paths = [ln.split()[-1] for ln in maps if "/libamdhip64.so" in ln]
+        if not paths:
+            raise RuntimeError("the HIP runtime is not loaded in this process")
+        hip = ctypes.CDLL(paths[0])
         hip.hipGraphUpload.restype = ctypes.c_int
         hip.hipGraphUpload.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
         _hip_runtime = hip
