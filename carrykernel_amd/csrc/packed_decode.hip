@@ -217,7 +217,9 @@ extern "C" int ck_gdn_packed_decode_to(const void* mixed_qkv, int qkv_dtype, int
                                        int use_qk_l2norm, int resid_fmt, int rscale_mode,
                                        int state_bits, int quant_mode,
                                        void* stream) {
-  if (!dst_state_indices) return ck::fail(CK_EINVAL, "dst_state_indices is NULL (use ck_gdn_packed_decode)");
+  // an empty batch (B = 0) may pass NULL id arrays, as an empty tensor's data pointer is
+  if (!dst_state_indices && B != 0)
+    return ck::fail(CK_EINVAL, "dst_state_indices is NULL (use ck_gdn_packed_decode)");
   return packed_decode_impl(mixed_qkv, qkv_dtype, stride_qkv_tok, a, a_dtype, stride_a_tok, b, b_dtype, stride_b_tok,
                             A_log, A_log_dtype, dt_bias, dt_bias_dtype, scale, state_codes, stride_state_slot,
                             state_scale, stride_sscale_slot, resid_codes, stride_resid_slot, resid_scale,

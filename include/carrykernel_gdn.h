@@ -101,8 +101,11 @@ int ck_abi_version(void);
  *   the masked kernel, which computes as if every row, q and k were
  *   zero-padded to max(16, next_pow2(K)), as the reference's masked lanes do
  *   (quantized_packed_decode.py:123-127,158,165-166,303), with whole 16-byte
- *   lane accesses when K is a multiple of 16 and rows are aligned, byte
- *   accesses otherwise.
+ *   lane accesses when K is a multiple of 16 and rows are aligned, 4- and
+ *   2-byte accesses when K is a multiple of 4 and rows are 4-byte aligned
+ *   (2-byte for int4 residual rows), byte accesses otherwise.
+ * B == 0 checks the sizes and codes, launches nothing and returns CK_OK; the
+ *   pointer arguments may then be NULL (an empty tensor's data pointer).
  */
 int ck_gdn_packed_decode(const void* mixed_qkv, int qkv_dtype, int64_t stride_qkv_tok,
                          const void* a, int a_dtype, int64_t stride_a_tok,
@@ -132,7 +135,8 @@ int ck_gdn_packed_decode(const void* mixed_qkv, int qkv_dtype, int64_t stride_qk
  * race. Chains of calls (token t reads the slot token t-1 wrote) keep every
  * intermediate state, which is what speculative decoding needs to roll back;
  * a shared prefix slot can be decoded into a request's own slot without a
- * copy. dst_state_indices must not be NULL; quant_mode must be CK_QUANT_FAST
+ * copy. dst_state_indices must not be NULL unless B == 0 (as for
+ * ck_gdn_packed_decode, nothing is then launched); quant_mode must be CK_QUANT_FAST
  * (other modes return CK_EUNSUPPORTED).
  */
 int ck_gdn_packed_decode_to(const void* mixed_qkv, int qkv_dtype, int64_t stride_qkv_tok,

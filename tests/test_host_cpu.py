@@ -78,6 +78,21 @@ def test_packed_decode_empty_batch_is_ok(L):
     assert L.ck_last_error().decode() == ""
 
 
+def test_packed_decode_empty_batch_with_null_pointers(L):
+    """B = 0 with every pointer NULL (an empty tensor's data pointer): the
+    in-place and the out-of-place step return CK_OK and launch nothing; with
+    B > 0 a NULL destination id array is refused."""
+    nulls = {k: None for k in ("mixed", "a", "b", "A_log", "dt_bias", "state", "sscale", "resid", "rscale",
+                               "out", "idx")}
+    at = 26   # ck_gdn_packed_decode_to takes (dst ids, stride) after (ids, stride)
+    args = _pd_args(B=0, **nulls)
+    assert L.ck_gdn_packed_decode(*args) == _native.CK_OK
+    assert L.ck_gdn_packed_decode_to(*args[:at], None, 1, *args[at:]) == _native.CK_OK
+    args = _pd_args()
+    assert L.ck_gdn_packed_decode_to(*args[:at], None, 1, *args[at:]) == _native.CK_EINVAL
+    assert "dst_state_indices is NULL" in L.ck_last_error().decode()
+
+
 def test_other_entry_points_argument_errors(L):
     p = ctypes.c_void_p(16)
     rc = L.ck_gdn_quant_step(p, p, p, p, p, p, p, p, p, p, p, p, p, p, 1, 1, 24, 8, 127.0, 0, 0, None)

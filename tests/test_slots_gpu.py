@@ -191,3 +191,28 @@ def test_preemption_swap_resumes_bit_exact(device):
         np.testing.assert_array_equal(o1, o2)
     for x, y in zip(run, ref):
         torch.testing.assert_close(x[[6, 3]], y[[2, 5]], rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("resid_fmt", [qpd.RESID_INT8, qpd.RESID_INT4])
+def test_empty_batch_touches_nothing(device, resid_fmt):
+    """B = 0 (no request in this step): the decode in place and out of place,
+    and the copy and reset of zero slots, return at once and leave every byte
+    of the pool as it was."""
+    H = HV = 4
+    K = V = 32
+    hpool = make_pool(5, HV, V, K, resid_fmt, False, seed=5)
+    dpool = to_dev(hpool, device)
+    mixed = torch.zeros(0, 2 * H * K + HV * V, device=device)
+    a, b = torch.zeros(0, HV, device=device), torch.zeros(0, HV, device=device)
+    A_log, dt_bias = torch.zeros(HV, device=device), torch.zeros(HV, device=device)
+    out = torch.empty(0, 1, HV, V, device=device)
+    none = _ids([], device)
+    got = qpd.quantized_gated_delta_rule_packed_decode(mixed, a, b, A_log, dt_bias, 1.0, *dpool, out, none,
+                                                       resid_fmt=resid_fmt)
+    assert got.shape == (0, 1, HV, V)
+    qpd.quantized_gated_delta_rule_packed_decode(mixed, a, b, A_log, dt_bias, 1.0, *dpool, out, none,
+                                                 resid_fmt=resid_fmt, dst_state_indices=none)
+    qpd.copy_quantized_state(dpool, none, dpool, none)
+    qpd.reset_quantized_state(dpool, none)
+    torch.cuda.synchronize()
+    _assert_pool(dpool, hpool, "after B = 0 calls")

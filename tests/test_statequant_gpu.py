@@ -316,3 +316,26 @@ def test_native_module_boundary(device, res_fmt):
     assert torch.equal(h_out, ref_h) and torch.equal(o, ref_o)
     with pytest.raises(RuntimeError, match="h_in must be fp32"):
         ext.gdn_fp32_step(d[0], *d[4:], o, h_out, 128)
+
+
+@pytest.mark.parametrize("res_fmt", [sq.RES_FP32, sq.RES_INT8])
+def test_empty_batch(device, res_fmt):
+    """B = 0: the fused step (front end and binding) and the fp32 step return
+    empty outputs of the right shapes without launching anything."""
+    HV, K, V = 4, 32, 64
+    codes = torch.zeros(0, HV, K, V, dtype=torch.int8, device=device)
+    scale = torch.zeros(0, HV, V, device=device)
+    e = torch.zeros(0, HV, K, V, dtype=sq.residual_dtype(res_fmt), device=device)
+    es = torch.zeros(0, HV, V, device=device) if res_fmt == sq.RES_INT8 else None
+    q, k = torch.zeros(0, HV, K, device=device), torch.zeros(0, HV, K, device=device)
+    v = torch.zeros(0, HV, V, device=device)
+    alpha, beta = torch.zeros(0, HV, device=device), torch.zeros(0, HV, device=device)
+    for step in (sq.gdn_quant_step_fused, binding.gdn_quant_step_hip):
+        o, h, s, e_new, es_new = step(codes, scale, e, es, q, k, v, alpha, beta, 8, res_fmt)
+        assert o.shape == (0, HV, V) and s.shape == (0, HV, V)
+        assert h.shape == (0, HV, K, V) and h.dtype == torch.int8
+        assert e_new.shape == (0, HV, K, V) and e_new.dtype == e.dtype
+        assert (es_new is None) == (res_fmt != sq.RES_INT8)
+    h_out, o = sq.gdn_step_fused_fp32(torch.zeros(0, HV, K, V, device=device), q, k, v, alpha, beta)
+    assert h_out.shape == (0, HV, K, V) and o.shape == (0, HV, V)
+    torch.cuda.synchronize()
