@@ -34,6 +34,9 @@ CASES = {
     "k24_int4_head": (24, 4, 2, 4, 40, I4, True, "fast", F32, F32, True, 0.0, False, False, 8, 2, False),
     "k7_int8_head_exact": (7, 3, 1, 2, 33, I8, True, "exact", F32, F32, True, 0.0, False, False, 8, 2, False),
     "k2_int4_row": (2, 5, 2, 2, 17, I4, False, "fast", F32, F32, False, 0.0, False, False, 8, 3, False),
+    # the smallest shapes: one code per row, one row per head
+    "k1_v1_int8_row": (1, 3, 1, 2, 1, I8, False, "fast", F32, F32, True, 0.0, False, False, 8, 3, False),
+    "k1_v3_int8_head_exact": (1, 4, 2, 2, 3, I8, True, "exact", F32, F32, False, 0.25, False, False, 8, 2, False),
     "k100_int8_row_bf16_nulls": (100, 8, 2, 4, 64, I8, False, "fast", BF16, BF16, True, 0.25, True, False, 8, 2,
                                  False),
     "k200_int4_head_gqa": (200, 4, 2, 6, 96, I4, True, "fast", F32, F32, True, 0.0, False, False, 8, 2, False),

@@ -60,10 +60,11 @@ def _random_state(B, HV, K, V, res_fmt, seed, bits=8):
 @pytest.mark.parametrize("mode", ["fast", "exact"])
 @pytest.mark.parametrize("K,V,B,HV", [(128, 128, 2, 32), (64, 64, 1, 4), (32, 8, 1, 1), (16, 136, 2, 3),
                                      (256, 128, 1, 4), (128, 130, 1, 3), (256, 130, 2, 2), (16, 3, 2, 2),
-                                     (64, 67, 1, 2)])
+                                     (64, 67, 1, 2), (16, 1, 3, 1)])
 def test_step_bit_exact_vs_oracle(device, res_fmt, mode, K, V, B, HV):
-    """K = 256 runs 16 slices of 16 rows; V not a multiple of 4 (130, 3, 67)
-    takes the per-column access path with a partial last column group."""
+    """K = 256 runs 16 slices of 16 rows; V not a multiple of 4 (130, 3, 67,
+    and a single column) takes the per-column access path with a partial last
+    column group."""
     h_int8, scale, e, es = _random_state(B, HV, K, V, res_fmt, seed=K + V + res_fmt)
     _, q, k, v, alpha, beta = make_inputs(1, B, HV, K, V, seed=5)
     beta = beta[0] * 0 + torch.rand(B, HV, generator=torch.Generator().manual_seed(9))
