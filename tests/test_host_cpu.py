@@ -202,6 +202,9 @@ def test_qpd_no_cpu_fallback():
 def test_statequant_shape_errors():
     B, HV, K, V = 1, 2, 32, 8
     z = torch.zeros
+    for bad in (z(5), z(2, 0, V), z(2, K, 0)):
+        with pytest.raises(ValueError):
+            sq.per_v_channel_quantize(bad)
     with pytest.raises(AssertionError):
         sq.gdn_quant_step_fused(z(B, HV, K, V), z(B, HV, V), z(B, HV, K, V), None, z(B, HV, K), z(B, HV, K),
                                 z(B, HV, V), z(B, HV), z(B, HV))
