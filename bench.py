@@ -369,29 +369,38 @@ def _graph_upload(graph, device):
 
 class StepReplayer:
     """Exactly `warmup` untimed launches of step(t), then exactly `steps`
-    timed ones, all graph-replayed. Every graph is captured and uploaded when
-    the replayer is built, so nothing is captured between the warm-up and the
-    timed region and no graph's first replay is timed. The warm-up is
-    warmup // period replays of a graph of steps 0 .. period-1 plus one graph
-    of the remainder; the timed steps are replays of one graph of
-    min(steps, MAX_GRAPH_STEPS) steps plus one graph of the remainder, so a
-    short run is one or two graph launches."""
+    timed ones, all graph-replayed, with t running on from the warm-up into
+    the timed region: the warm-up runs t = 0 .. warmup-1 and the timed steps
+    t = warmup .. warmup+steps-1 (step(t) depends on t only modulo `period`),
+    so every timed step's slot group was last touched `period` steps earlier,
+    never a few steps earlier by the warm-up. Every graph is captured and
+    uploaded when the replayer is built, so nothing is captured between the
+    warm-up and the timed region and no graph's first replay is timed. The
+    warm-up is warmup // period replays of a graph of steps 0 .. period-1 plus
+    one graph of the remainder; the timed steps are replays of one graph of
+    at most MAX_GRAPH_STEPS steps (a multiple of `period` when there is more
+    than one replay, so each replay ends where the next begins in the
+    rotation) plus one graph of the remainder, so a short run is one graph
+    launch."""
 
     MAX_GRAPH_STEPS = 1024
 
     def __init__(self, device, step, period, steps, warmup):
         self.device, self.steps, self.warmup = device, steps, warmup
 
-        def graph(n):
-            return _graph_upload(_capture(device, step, range(n)), device) if n > 0 else None
+        def graph(t0, n):
+            return _graph_upload(_capture(device, step, range(t0, t0 + n)), device) if n > 0 else None
 
-        self.warm_full = graph(period) if warmup >= period else None
+        self.warm_full = graph(0, period) if warmup >= period else None
         self.warm_reps = warmup // period
-        self.warm_tail = graph(warmup % period)
-        n_big = min(steps, self.MAX_GRAPH_STEPS)
-        self.big = graph(n_big)
+        self.warm_tail = graph(0, warmup % period)
+        if steps <= self.MAX_GRAPH_STEPS:
+            n_big = steps
+        else:
+            n_big = max(period, self.MAX_GRAPH_STEPS - self.MAX_GRAPH_STEPS % period)
+        self.big = graph(warmup, n_big)
         self.big_reps = steps // n_big if n_big > 0 else 0
-        self.tail = graph(steps - self.big_reps * n_big)
+        self.tail = graph(warmup + self.big_reps * n_big, steps - self.big_reps * n_big)
 
     def time_ms_per_step(self):
         """The warm-up, a synchronize, then the timed steps between two HIP

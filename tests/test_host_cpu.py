@@ -316,22 +316,27 @@ def test_bench_refuses_more_than_one_gpu():
 
 
 @pytest.mark.parametrize("steps,warmup,period", [(20, 5, 16), (2000, 200, 16), (1, 0, 16), (1024, 16, 16),
-                                                 (1025, 17, 16), (3000, 3, 8), (16, 15, 16)])
+                                                 (1025, 17, 16), (3000, 3, 8), (16, 15, 16), (3000, 7, 12),
+                                                 (2100, 30, 100)])
 def test_bench_times_exactly_k_steps(monkeypatch, steps, warmup, period):
     """The bench's replayer runs exactly `warmup` steps before the start
     event, exactly `steps` steps between the two events and nothing after; the
     timed steps are at most ceil(steps / 1024) + 1 graph launches, and every
-    graph is captured (and uploaded) before the warm-up."""
+    graph is captured (and uploaded) before the warm-up. The step indices
+    run on from the warm-up into the timed region, modulo the rotation
+    period: the warm-up replays t = 0 .. warmup-1 and the timed region
+    t = warmup .. warmup+steps-1, so no timed step re-reads a slot group that
+    the warm-up touched fewer than `period` steps before."""
     import bench
     log, marks = [], {}
 
     class FakeGraph:
-        def __init__(self, n):
-            self.n = n
+        def __init__(self, ts):
+            self.ts = list(ts)
             marks.setdefault("captures_at", []).append(len(log))
 
         def replay(self):
-            log.append(self.n)
+            log.extend(self.ts)
 
     class FakeTimer:
         def __init__(self, device):
@@ -344,17 +349,27 @@ def test_bench_times_exactly_k_steps(monkeypatch, steps, warmup, period):
             marks["stop"] = len(log)
             return 1.0
 
-    monkeypatch.setattr(bench, "_capture", lambda device, step, ts: FakeGraph(len(ts)))
+    launches = []
+    real_replay = FakeGraph.replay
+
+    def counting_replay(self):
+        launches.append(len(log))
+        real_replay(self)
+
+    FakeGraph.replay = counting_replay
+    monkeypatch.setattr(bench, "_capture", lambda device, step, ts: FakeGraph(ts))
     monkeypatch.setattr(bench, "_graph_upload", lambda graph, device: graph)
     monkeypatch.setattr(bench, "Timer", FakeTimer)
     monkeypatch.setattr(bench.torch.cuda, "synchronize", lambda *a, **k: None)
     rep = bench.StepReplayer("cpu", None, period, steps, warmup)
     ms = rep.time_ms_per_step()
     assert all(at == 0 for at in marks["captures_at"])
-    assert sum(log[:marks["start"]]) == warmup
-    assert sum(log[marks["start"]:marks["stop"]]) == steps
+    assert marks["start"] == warmup
+    assert marks["stop"] - marks["start"] == steps
     assert len(log) == marks["stop"]
-    assert marks["stop"] - marks["start"] <= -(-steps // bench.StepReplayer.MAX_GRAPH_STEPS) + 1
+    assert [t % period for t in log] == [t % period for t in range(warmup + steps)]
+    timed_launches = sum(1 for at in launches if at >= marks["start"])
+    assert timed_launches <= -(-steps // bench.StepReplayer.MAX_GRAPH_STEPS) + 1
     assert ms == pytest.approx(1.0 / steps)
 
 
