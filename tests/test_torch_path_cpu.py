@@ -96,15 +96,21 @@ def test_torch_path_agrees_with_oracle(fmt, per_head):
     moves one element by a whole LSB; codes plus residual reconstruct the
     same state to ~1e-5), state codes off by one on a few elements per
     million, state scales within a few ulp, residual scales to 1e-4
-    relative."""
+    relative. The bounds sit just above what these four configurations
+    measure (B=8, H=HV=32, K=V=128, seed 0), so that a change in either
+    mode's arithmetic shows here: state scales at most 4 ulp apart in both
+    modes (measured 4), more than 1 ulp apart on at most 1.5 % of rows for
+    EXACT (measured 1.10-1.13 %) and 2.5 % for FAST (2.10-2.12 %); state
+    codes flipped on at most 5e-6 of elements (EXACT <= 9.5e-7, FAST <=
+    3.3e-6); residual scales within 1e-4 relative (<= 8.2e-5)."""
     res = _three_ways(fmt, per_head)
-    for name in ("exact", "fast"):
+    for name, over_1ulp in (("exact", 0.015), ("fast", 0.025)):
         d = _agreement(res[name], res["torch"], fmt)
         print(name, "vs torch:", d)
         assert d["o_rel"] < 2e-6 and d["deq_rel"] < 1e-4 and d["recon_rel"] < 1e-4
-        assert d["code_max"] <= 1 and d["code_flip"] <= 1e-5
+        assert d["code_max"] <= 1 and d["code_flip"] <= 5e-6
         assert d["resid_code_ok"] and d["resid_flip"] <= 1e-3
-        assert d["sscale_ulp_max"] <= 16 and d["sscale_over_1ulp"] <= 0.05
+        assert d["sscale_ulp_max"] <= 4 and d["sscale_over_1ulp"] <= over_1ulp
         assert d["rscale_rel"] < 1e-4
 
 
