@@ -293,7 +293,8 @@ class CpuLeg:
         run()
         torch.cuda.synchronize()
         xk = self._host(x.reshape(-1, x.shape[-1])[:rows])
-        c_ref, s_ref = orc.quantize_rows(xk, qmax)
+        name_of = {torch.float32: "float32", torch.bfloat16: "bfloat16", torch.float16: "float16"}
+        c_ref, s_ref = orc.quantize_rows_in_dtype(xk, name_of[x.dtype], qmax)
         ok = np.array_equal(self._host(codes.reshape(-1, x.shape[-1])[:rows]), c_ref) and \
             np.array_equal(self._host(scale.reshape(-1)[:rows]), s_ref)
         return self._record(name, ok, "" if ok else "row ingest differs")

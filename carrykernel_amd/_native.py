@@ -33,6 +33,7 @@ CK_ELAUNCH = 3
 
 # enum ck_dtype
 DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+DTYPE_F64 = 3  # CK_DTYPE_F64: ck_quantize_rows only
 
 # enum ck_res_fmt / ck_resid_fmt / ck_rscale_mode / ck_quant_mode
 QUANT_FAST = 0

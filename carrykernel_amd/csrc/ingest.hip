@@ -1,7 +1,14 @@
 // State ingest: quantize a float state into the int8 pool.
 //   ck_quantize_rows: rows of K (vLLM [.., V, K] layout), one scale per row,
 //     init_quantized_state semantics (vllm_integration/quantized_packed_decode.py:347-351):
-//     scale = max(amax, 1e-12) / qmax, code = clamp(rne(x / scale), +-qmax).
+//     scale = max(amax, 1e-12) / qmax, code = clamp(rne(x / scale), +-qmax),
+//     evaluated in the precision of x as torch evaluates that expression on a
+//     tensor of x's dtype: fp32 and float64 arithmetic as such; for bf16 and
+//     fp16 every operation is computed in fp32 and rounded (to nearest even)
+//     to x's dtype, so the scale is the 16-bit value RN16(RN(max(amax, RN16(
+//     1e-12)) / qmax)) and the quotient RN16(RN(x / scale)) is rounded to an
+//     integer from there (it can reach qmax + 1 in bf16, where the clamp then
+//     binds). A float64 scale is stored rounded to fp32.
 //   ck_quantize_cols: [K, V] matrices, one scale per V-column (amax over K),
 //     per_v_channel_quantize semantics (statequant/kernel.py:99-113).
 // Both divide correctly rounded (IEEE division, or the reciprocal with
@@ -16,6 +23,32 @@
 
 namespace ck {
 namespace {
+
+// x rounded to nearest even to the 16-bit dtype DT and back to fp32 (fp32:
+// unchanged); subnormal fp16 results are kept (the conversion honours fp16
+// denormals), values past the largest finite fp16 become inf.
+template <int DT>
+__device__ __forceinline__ float round16(float x) {
+  if constexpr (DT == kBF16) {
+    return bf16_to_f32(f32_to_bf16_rne(x));
+  } else if constexpr (DT == kF16) {
+    return (float)(_Float16)x;
+  } else {
+    return x;
+  }
+}
+
+__device__ __forceinline__ float round16_rt(int dt, float x) {
+  return dt == kBF16 ? round16<kBF16>(x) : dt == kF16 ? round16<kF16>(x) : x;
+}
+
+// RN(t / s) from inv = RN(1 / s) by Markstein's correction (the EXACT quotient
+// of ck_quant.h, before its rounding to an integer).
+__device__ __forceinline__ float quantize_quotient(float t, float s, float inv) {
+  const float q0 = t * inv;
+  const float r = fmaf(-q0, s, t);
+  return fmaf(r, inv, q0);
+}
 
 // Rows of K = 16 * LPR (K <= 256), 16-byte aligned: a lane owns 16 consecutive
 // elements of a row (vector loads, one 16-byte store of codes), the LPR lanes
@@ -66,11 +99,32 @@ __global__ __launch_bounds__(256) void quantize_rows16_kernel(const char* __rest
 #pragma unroll
     for (int j = 1; j < 16; ++j) am = fmaxf(am, fabsf(v[j]));
     am = group_max<LPR>(am);
-    const float s = fmaxf(am, kEps) / qmax;
-    const float inv = recip_rn(s);
     uint32_t yb[16];
+    float s;
+    if constexpr (DT == kF32) {
+      s = fmaxf(am, kEps) / qmax;
+      const float inv = recip_rn(s);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) (void)quantize<kExact>(v[j], s, inv, yb[j]);
+      for (int j = 0; j < 16; ++j) (void)quantize<kExact>(v[j], s, inv, yb[j]);
+    } else {
+      // in x's precision: RN16 after every fp32 operation (see the header)
+      s = round16<DT>(fmaxf(am, round16<DT>(kEps)) / qmax);
+      if (s > 0.0f) {
+        const float inv = recip_rn(s);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const float q = round16<DT>(quantize_quotient(v[j], s, inv));
+          yb[j] = __float_as_uint(fminf(fmaxf(rintf(q), -qmax), qmax) + kMagic);
+        }
+      } else {
+        // fp16 only (RN16(1e-12) = 0): the row's scale rounded to 0, so x / 0
+        // is +-inf (clamped to +-qmax) for x != 0 and NaN for x = 0, which
+        // the reference's int8 conversion turns into 0
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          yb[j] = __float_as_uint((v[j] > 0.0f ? qmax : v[j] < 0.0f ? -qmax : 0.0f) + kMagic);
+      }
+    }
     if (valid) {
       __builtin_nontemporal_store(u32x4{pack_low_bytes(yb[0], yb[1], yb[2], yb[3]),
                                         pack_low_bytes(yb[4], yb[5], yb[6], yb[7]),
@@ -101,7 +155,8 @@ void launch_rows16(const void* x, int dtype, int64_t stride_row, int64_t rows, f
                        stride_row * esz, rows, qmax, codes, scale);
 }
 
-// Any K, any alignment: one wavefront per row; lanes stride over K.
+// Any K, any alignment: one wavefront per row; lanes stride over K. 16-bit
+// dtypes in their own precision (RN16 after each fp32 operation).
 __global__ __launch_bounds__(256) void quantize_rows_kernel(const void* __restrict__ x, int dtype, int64_t stride_row,
                                                             int64_t rows, int K, float qmax,
                                                             int8_t* __restrict__ codes, float* __restrict__ scale) {
@@ -112,12 +167,35 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const void* __restri
   float am = 0.0f;
   for (int j = lane; j < K; j += 64) am = fmaxf(am, fabsf(load_act(x, base + j, dtype)));
   am = wave_max(am);
-  const float s = fmaxf(am, kEps) / qmax;
+  const float s = round16_rt(dtype, fmaxf(am, round16_rt(dtype, kEps)) / qmax);
   for (int j = lane; j < K; j += 64) {
-    const float c = fminf(fmaxf(rintf(load_act(x, base + j, dtype) / s), -qmax), qmax);
+    // IEEE division: an fp16 scale that rounded to 0 gives +-inf (clamped to
+    // +-qmax) for x != 0 and NaN for x = 0, which the int8 conversion of the
+    // reference turns into 0
+    const float q = round16_rt(dtype, load_act(x, base + j, dtype) / s);
+    const float c = q != q ? 0.0f : fminf(fmaxf(rintf(q), -qmax), qmax);
     codes[row * K + j] = (int8_t)(int)c;
   }
   if (lane == 0) scale[row] = s;
+}
+
+// float64 rows (any K, alignment of a double): one wavefront per row, the
+// arithmetic in float64 as torch does for a float64 h0; the scale is stored
+// rounded to fp32 (the pool's scale dtype), the codes use the float64 scale.
+__global__ __launch_bounds__(256) void quantize_rows_f64_kernel(const double* __restrict__ x, int64_t stride_row,
+                                                                int64_t rows, int K, double qmax,
+                                                                int8_t* __restrict__ codes, float* __restrict__ scale) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // whole wavefront exits together
+  const double* xr = x + row * stride_row;
+  double am = 0.0;
+  for (int j = lane; j < K; j += 64) am = fmax(am, fabs(xr[j]));
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) am = fmax(am, __shfl_xor(am, m, 64));
+  const double s = fmax(am, 1e-12) / qmax;
+  for (int j = lane; j < K; j += 64) codes[row * K + j] = (int8_t)(int)fmin(fmax(rint(xr[j] / s), -qmax), qmax);
+  if (lane == 0) scale[row] = (float)s;
 }
 
 // [M, K, V] matrices with K in {16, 32, 64, 128, 256}, V % 4 == 0, 16-byte aligned:
@@ -194,11 +272,19 @@ extern "C" int ck_quantize_rows(const void* x, int x_dtype, int64_t stride_row, 
                                 int8_t* codes, float* scale, void* stream) {
   using namespace ck;
   if (rows < 0 || K <= 0 || stride_row < K) return fail(CK_EINVAL, "bad sizes rows=%lld K=%d", (long long)rows, K);
-  if (!valid_dtype(x_dtype)) return fail(CK_EINVAL, "unsupported dtype code %d", x_dtype);
+  if (!valid_dtype(x_dtype) && x_dtype != CK_DTYPE_F64) return fail(CK_EINVAL, "unsupported dtype code %d", x_dtype);
   if (!(qmax >= 1.0f && qmax <= 127.0f)) return fail(CK_EINVAL, "qmax must be in [1, 127]");
   if (rows == 0) return ok();
   if (!x || !codes || !scale) return fail(CK_EINVAL, "null pointer argument");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (x_dtype == CK_DTYPE_F64) {
+    if (reinterpret_cast<uintptr_t>(x) & 7) return fail(CK_EINVAL, "float64 rows must be 8-byte aligned");
+    const int64_t grid = (rows + 3) / 4;
+    if (grid > 0x7fffffff) return fail(CK_EUNSUPPORTED, "too many rows");
+    hipLaunchKernelGGL(quantize_rows_f64_kernel, dim3((unsigned)grid), dim3(256), 0, s, static_cast<const double*>(x),
+                       stride_row, rows, K, (double)qmax, codes, scale);
+    return check_launch("ck_quantize_rows");
+  }
   const int esz = x_dtype == kF32 ? 4 : 2;
   const bool aligned = ((reinterpret_cast<uintptr_t>(x) | (uintptr_t)(stride_row * esz) |
                          reinterpret_cast<uintptr_t>(codes)) & 15) == 0;

@@ -379,11 +379,14 @@ def init_quantized_state(num_slots: int, HV: int, V: int, K: int, device,
     """Allocate the quantized state pool, optionally seeding slot contents.
 
     quantized_packed_decode.py:330-352. ``h0``, when given, is
-    ``[num_slots, HV, V, K]`` in any floating dtype on any device (float64 is
-    read as fp32, a host tensor is copied to ``device``) and is quantized into
-    the pool on the GPU (``ck_quantize_rows``: scale = max(amax_K, eps) / qmax,
-    codes = rne(h0 / scale)); the residual starts at zero. Returns
-    ``(state_codes, state_scale, resid_codes, resid_scale)``.
+    ``[num_slots, HV, V, K]`` in a floating dtype on any device (a host
+    tensor is copied to ``device``) and is quantized into the pool on the GPU
+    (``ck_quantize_rows``: scale = max(amax_K, eps) / qmax, codes =
+    clamp(rne(h0 / scale))) in h0's own precision, as the reference's torch
+    expression computes it: fp32 and float64 as such (a float64 scale is
+    stored rounded to fp32), bf16 and fp16 with every operation rounded to
+    that dtype; other floating dtypes are read as fp32. The residual starts at
+    zero. Returns ``(state_codes, state_scale, resid_codes, resid_scale)``.
     ``per_head_resid_scale`` allocates ``resid_scale`` as ``[num_slots, HV]``.
     """
     device = torch.device(device)
@@ -404,14 +407,19 @@ def init_quantized_state(num_slots: int, HV: int, V: int, K: int, device,
     if h0 is not None:
         # h0 may come from any device and in any float dtype, as the
         # reference's (quantized_packed_decode.py:347-351 quantizes in h0's
-        # precision and copy_()s into the pool): move it to the pool's GPU,
-        # and narrow dtypes the kernel does not read (float64) to fp32.
-        if h0.dtype not in (torch.float32, torch.bfloat16, torch.float16):
-            h0 = h0.to(torch.float32)
+        # precision and copy_()s into the pool): move it to the pool's GPU;
+        # the kernel reads fp32, bf16, fp16 and float64 in their own
+        # precision, other floating dtypes are read as fp32.
+        if h0.dtype == torch.float64:
+            code = _native.DTYPE_F64
+        else:
+            if h0.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+                h0 = h0.to(torch.float32)
+            code = _native.dtype_code(h0, "h0")
         h0 = h0.to(device).contiguous()
         qmax = float(2 ** (int(state_bits) - 1) - 1)
         L = _native.lib()
-        status = L.ck_quantize_rows(h0.data_ptr(), _native.dtype_code(h0, "h0"), K,
+        status = L.ck_quantize_rows(h0.data_ptr(), code, K,
                                     num_slots * HV * V, K, qmax,
                                     state_codes.data_ptr(), state_scale.data_ptr(),
                                     _native.stream_handle(device))

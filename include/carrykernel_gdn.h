@@ -51,8 +51,9 @@ enum ck_status {
   CK_ELAUNCH = 3       /* the HIP runtime rejected the kernel launch            */
 };
 
-/* Element types of activations / outputs / float state. */
-enum ck_dtype { CK_DTYPE_F32 = 0, CK_DTYPE_BF16 = 1, CK_DTYPE_F16 = 2 };
+/* Element types of activations / outputs / float state. CK_DTYPE_F64 is
+ * accepted by ck_quantize_rows only (a float64 prefill state). */
+enum ck_dtype { CK_DTYPE_F32 = 0, CK_DTYPE_BF16 = 1, CK_DTYPE_F16 = 2, CK_DTYPE_F64 = 3 };
 
 /* Residual formats of the vLLM-layout path (quantized_packed_decode.py:82-83). */
 enum ck_resid_fmt { CK_RESID_INT8 = 0, CK_RESID_INT4 = 1 };
@@ -237,8 +238,15 @@ int ck_gdn_fp32_step(const float* h_in, const float* q, const float* k, const fl
 /*
  * Quantize rows of length K (contiguous, row stride `stride_row` elements) to
  * int8 codes with one scale per row: scale = max(amax, 1e-12) / qmax,
- * code = rne(x / scale) clamped to +-qmax (init_quantized_state semantics).
- * codes are written contiguous [rows, K], scales [rows].
+ * code = rne(x / scale) clamped to +-qmax (init_quantized_state semantics,
+ * vllm_integration/quantized_packed_decode.py:347-351), evaluated in x's
+ * precision as torch evaluates that expression on a tensor of x's dtype:
+ * fp32 / float64 arithmetic for CK_DTYPE_F32 / CK_DTYPE_F64 (the float64
+ * scale is stored rounded to fp32); for CK_DTYPE_BF16 / CK_DTYPE_F16 every
+ * operation in fp32 rounded to nearest even to x's dtype (the scale is then
+ * a bf16 / fp16 value, the quotient is rounded to x's dtype before rne, and
+ * the clamp can bind). An fp16 row whose scale rounds to 0 (all zeros) gets
+ * codes 0. codes are written contiguous [rows, K], scales [rows].
  */
 int ck_quantize_rows(const void* x, int x_dtype, int64_t stride_row, int64_t rows, int K,
                      float qmax, int8_t* codes, float* scale, void* stream);

@@ -178,6 +178,43 @@ def quantize_rows(x, qmax=127.0):
     return codes, scale
 
 
+def quantize_rows_in_dtype(x, dtype: str, qmax=127.0):
+    """init_quantized_state seeding (quantized_packed_decode.py:347-351) of an
+    h0 of dtype "float32", "bfloat16", "float16" or "float64", in that dtype's
+    precision as torch evaluates ``scale = h0.abs().amax(-1).clamp(min=1e-12)
+    / qmax; codes = torch.round(h0 / scale).clamp(-qmax, qmax).to(int8)``:
+    for the 16-bit dtypes each operation in fp32, rounded to nearest even to
+    the dtype (numpy float16 for fp16, ``bf16_round`` for bf16); float64 in
+    float64, its scale then rounded to fp32 as ``state_scale.copy_`` does.
+    ``x`` holds the h0 values (exactly representable in ``dtype``). NaN
+    quotients (0 / 0 when an fp16 scale rounds to 0) become code 0, as the
+    int8 conversion gives them. Pure numpy."""
+    if dtype == "float32":
+        return quantize_rows(x, qmax)
+    if dtype == "float64":
+        xd = np.asarray(x, np.float64)
+        s = np.maximum(np.abs(xd).max(axis=-1), 1e-12) / float(qmax)
+        with np.errstate(invalid="ignore", divide="ignore"):
+            q = np.clip(np.rint(xd / s[..., None]), -qmax, qmax)
+        return q.astype(np.int8), s.astype(np.float32)
+    if dtype == "bfloat16":
+        r16 = bf16_round
+    elif dtype == "float16":
+        def r16(v):
+            return np.asarray(v, np.float32).astype(np.float16).astype(np.float32)
+    else:
+        raise ValueError(f"unsupported dtype {dtype}")
+    xf = np.asarray(x, np.float32)
+    assert np.array_equal(r16(xf), xf), "x must hold values of the dtype"
+    eps = r16(np.float32(1e-12))
+    s = r16(np.maximum(np.abs(xf).max(axis=-1), eps) / np.float32(qmax))
+    with np.errstate(invalid="ignore", divide="ignore", over="ignore"):
+        q = r16(xf / s[..., None])
+    q = np.where(np.isnan(q), np.float32(0), q)
+    codes = np.clip(np.rint(q), -qmax, qmax).astype(np.int8)
+    return codes, s.astype(np.float32)
+
+
 def quantize_cols(x, qmax=127.0):
     """per_v_channel_quantize (statequant/kernel.py:99-113): [..., K, V], amax over K."""
     x = _f32(x)

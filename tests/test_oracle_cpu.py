@@ -560,6 +560,47 @@ def test_quantize_rows_cols_match_torch_round():
     np.testing.assert_array_equal(c2, torch.round(x / s_t2[..., None, :]).clamp(-127, 127).to(torch.int8).numpy())
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float64, torch.float32])
+@pytest.mark.parametrize("qmax", [127, 31])
+def test_quantize_rows_in_dtype_matches_torch_formula(dtype, qmax):
+    """oracle.quantize_rows_in_dtype against the reference's expression
+    (quantized_packed_decode.py:347-351: clamp(amax, 1e-12) / qmax, then
+    torch.round(h0 / scale).clamp(-qmax, qmax)) evaluated by torch in h0's own
+    dtype, bit for bit, on rows that exercise the dtype's corners: all-zero
+    rows (fp16: 1e-12 rounds to 0, so 0 / 0), one dominant value, tiny
+    magnitudes (fp16 subnormal scales, and fp16 scales that round to 0 under
+    nonzero values, whose quotients are +-inf and clamp to +-qmax) and many
+    rows whose bf16 quotient rounds past qmax (the clamp binds). For the
+    16-bit dtypes the in-dtype codes differ from quantizing the same values
+    in fp32, so the check has teeth."""
+    g = torch.Generator().manual_seed(qmax)
+    x = torch.randn(64, 4, 128, generator=g, dtype=torch.float64) * 0.3
+    x[0, 0] = 0.0
+    x[1, 1, 5] = 50.0
+    x[2] *= 3e-3
+    x[3, :, ::2] *= 1e-30
+    x[4] *= 1e-6
+    x = x.to(dtype)
+    name = {torch.bfloat16: "bfloat16", torch.float16: "float16", torch.float64: "float64",
+            torch.float32: "float32"}[dtype]
+    vals = x.numpy() if dtype == torch.float64 else x.float().numpy()
+    c, s = oracle.quantize_rows_in_dtype(vals, name, float(qmax))
+    s_t = x.abs().amax(dim=-1).clamp(min=1e-12) / qmax
+    c_t = torch.round(x / s_t[..., None]).clamp(-qmax, qmax).to(torch.int8).numpy()
+    np.testing.assert_array_equal(s, s_t.float().numpy())
+    np.testing.assert_array_equal(c, c_t)
+    if dtype in (torch.bfloat16, torch.float16):
+        c32, s32 = oracle.quantize_rows(x.float().numpy(), float(qmax))
+        assert not np.array_equal(c, c32) and not np.array_equal(s, s32)
+    if dtype == torch.bfloat16 and qmax == 127:
+        q = (x / s_t[..., None]).float()
+        assert int((torch.round(q).abs() > qmax).sum()) > 0   # the clamp binds
+    if dtype == torch.float16:
+        assert float(s_t[0, 0]) == 0.0 and np.all(c[0, 0] == 0)
+        assert np.any((s > 0) & (s < 6.1e-5))                 # subnormal fp16 scales
+        assert np.any(np.abs(c[4][s[4] == 0]) == qmax)        # scale 0 under nonzero values
+
+
 @pytest.mark.parametrize("K,V", [(64, 32), (256, 130)])
 def test_fp32_step_vs_float64(K, V):
     rng = np.random.default_rng(3)

@@ -16,8 +16,16 @@ pytestmark = pytest.mark.gpu
 MODES = {"fast": oracle.MODE_FAST, "exact": oracle.MODE_EXACT}
 
 
+def _normalize_qk(mixed, B, H, K):
+    """q and k of a packed row L2-normalised on the host (config C1-C5 inputs)."""
+    x = mixed.clone()
+    qk = x[:, :2 * H * K].view(B, 2 * H, K)
+    x[:, :2 * H * K] = (qk / qk.norm(dim=-1, keepdim=True)).reshape(B, -1)
+    return x
+
+
 def _run_both(device, B, H, HV, K, V, resid_fmt, per_head, mode, l2norm, T=1, seed=0,
-              act_dtype=torch.float32, out_dtype=torch.float32, bits=8, scale=None):
+              act_dtype=torch.float32, out_dtype=torch.float32, bits=8, scale=None, normalize_qk=False):
     """Run T steps on the GPU and in the oracle from the same pool; assert
     bit-exact agreement of every output after every step."""
     S = B + 3
@@ -29,6 +37,8 @@ def _run_both(device, B, H, HV, K, V, resid_fmt, per_head, mode, l2norm, T=1, se
     didx = torch.from_numpy(indices).to(device)
     for t in range(T):
         mixed, a, b, A_log, dt_bias = make_packed_inputs(B, H, HV, K, V, seed=1000 * seed + t, dtype=act_dtype)
+        if normalize_qk:
+            mixed = _normalize_qk(mixed.float(), B, H, K).to(act_dtype)
         out = torch.empty(B, 1, HV, V, dtype=out_dtype, device=device)
         print(f"case B={B} H={H} HV={HV} K={K} V={V} resid={resid_fmt} per_head={per_head} "
               f"mode={mode} l2={l2norm} t={t}", flush=True)
@@ -58,6 +68,17 @@ def _run_both(device, B, H, HV, K, V, resid_fmt, per_head, mode, l2norm, T=1, se
 def test_bit_exact_vs_oracle_k128(device, resid_fmt, per_head, mode):
     _run_both(device, B=4, H=32, HV=32, K=128, V=128, resid_fmt=resid_fmt, per_head=per_head,
               mode=mode, l2norm=False, T=3)
+
+
+@pytest.mark.parametrize("B", [1, 8])
+@pytest.mark.parametrize("mode", ["fast", "exact"])
+def test_c3_small_batches_bit_exact(device, B, mode):
+    """Config C3 at its small batches, on the config's shape: H = HV = 32,
+    K = V = 128, packed int4 residual with a per-head scale, q and k
+    normalised on the host (flag off, scale 1). B=1 runs one item per
+    workgroup on 32 CUs, B=8 256 items with no prefetch past the first."""
+    _run_both(device, B=B, H=32, HV=32, K=128, V=128, resid_fmt=qpd.RESID_INT4, per_head=True,
+              mode=mode, l2norm=False, T=3, seed=B, scale=1.0, normalize_qk=True)
 
 
 @pytest.mark.parametrize("resid_fmt", [qpd.RESID_INT8, qpd.RESID_INT4])
