@@ -422,14 +422,34 @@ class StepReplayer:
         return ms
 
 
+SLOT_ORDERS = ("random", "sorted", "dense")
+
+
+def slot_groups(S, B, groups, order, seed=0):
+    """The slot ids of each step's batch, `groups` disjoint groups of B ids
+    from 1 .. S-1 (slot 0 is the NULL block). random: a random permutation of
+    the pool cut into groups, request n reading a random slot (a long-running
+    server's slot map); sorted: the same groups, each in ascending slot
+    order; dense: group g is the consecutive slots g*B+1 .. (g+1)*B in
+    order (a freshly filled pool)."""
+    if order == "dense":
+        perm = torch.arange(1, S)
+    else:
+        perm = torch.randperm(S - 1, generator=torch.Generator().manual_seed(seed)) + 1
+    out = [perm[i * B:(i + 1) * B] for i in range(groups)]
+    if order == "sorted":
+        out = [torch.sort(g).values for g in out]
+    return [g.to(torch.int32) for g in out]
+
+
 def run_config(device, B, resid_fmt, per_head, steps, warmup, groups, quant_mode="fast", seed=0,
-               act_dtype=torch.float32, cpu=None, name=None):
+               act_dtype=torch.float32, cpu=None, name=None, slot_order="random"):
     """One configuration of the decode step: a pool of B * groups + 1 slots
     (state from 64 fp32 warm-up steps), each step on the next group of B
-    random slots. Returns {ms: device ms per step over exactly `steps`
-    graph-replayed steps, host_ms: host-inclusive ms per eager call,
-    validated: the CPU leg's bit-exact check of one step of this very
-    configuration (None without a CPU leg)}. `act_dtype` is the dtype of
+    slots (slot_groups: random by default). Returns {ms: device ms per step
+    over exactly `steps` graph-replayed steps, host_ms: host-inclusive ms per
+    eager call, validated: the CPU leg's bit-exact check of one step of this
+    very configuration (None without a CPU leg)}. `act_dtype` is the dtype of
     mixed_qkv, a, b and out (vLLM runs bf16 activations)."""
     S = B * groups + 1
     state = warm_state(S, device, seed)
@@ -439,8 +459,7 @@ def run_config(device, B, resid_fmt, per_head, steps, warmup, groups, quant_mode
     torch.cuda.empty_cache()
     sets, A_log, dt_bias = make_step_inputs(B, 8, device, seed + 1)
     sets = [tuple(x.to(act_dtype) for x in st) for st in sets]
-    perm = torch.randperm(S - 1, generator=torch.Generator().manual_seed(seed)) + 1
-    idx_groups = [perm[i * B:(i + 1) * B].to(torch.int32).to(device) for i in range(groups)]
+    idx_groups = [g.to(device) for g in slot_groups(S, B, groups, slot_order, seed)]
     out = torch.empty(B, 1, HV, V, device=device, dtype=act_dtype)
 
     def step(t):
@@ -983,6 +1002,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--groups", type=int, default=16, help="disjoint slot groups rotated over")
+    ap.add_argument("--slot-order", choices=SLOT_ORDERS, default="random",
+                    help="slot ids of each step's batch (slot_groups): random (default), sorted, dense")
     ap.add_argument("--resid", choices=("int4", "int8"), default="int4")
     ap.add_argument("--rscale", choices=("head", "row"), default="head")
     ap.add_argument("--quant-mode", choices=("fast", "exact"), default="fast")
@@ -1038,7 +1059,7 @@ def main():
 
     cpu = None if args.no_cpu else CpuLeg(args.cpu_seconds)
     r = run_config(device, B, resid_fmt, per_head, args.steps, args.warmup, args.groups, args.quant_mode,
-                   cpu=cpu, name=f"B{B}_{args.resid}_{args.rscale}_{args.quant_mode}")
+                   cpu=cpu, name=f"B{B}_{args.resid}_{args.rscale}_{args.quant_mode}", slot_order=args.slot_order)
     ms, host_ms = r["ms"], r["host_ms"]
     nbytes = algorithmic_bytes(B, H, HV, K, V, resid_fmt, per_head)
     gbps = nbytes / (ms * 1e-3) / 1e9
@@ -1061,7 +1082,7 @@ def main():
                                "(per-head scale), vLLM [slots,HV,V,K] layout",
                    "batch": B, "value_heads": HV, "qk_heads": H, "K": K, "V": V, "state": "int8",
                    "resid": args.resid, "resid_scale": args.rscale, "quant_mode": args.quant_mode,
-                   "pool_slots": B * args.groups + 1},
+                   "pool_slots": B * args.groups + 1, "slot_order": args.slot_order},
         "validated": r["validated"],
         "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,

@@ -419,3 +419,22 @@ def test_bench_float_state_step_passes_each_dtype_code(monkeypatch):
         bench.float_state_step(torch.zeros(3, HV_, V_, K_, dtype=torch.float16), mixed, a, b, A_log, dt, 1.0,
                                out, idx, False)
     assert len(calls) == 2
+
+
+def test_bench_slot_groups_orders():
+    """bench.slot_groups: every order gives `groups` disjoint batches of B
+    slot ids from 1 .. S-1 (never the NULL block 0); sorted holds the random
+    order's groups in ascending order; dense holds consecutive slots."""
+    import bench
+    S, B, groups = 4 * 16 + 1, 16, 4
+    rnd = bench.slot_groups(S, B, groups, "random", seed=3)
+    srt = bench.slot_groups(S, B, groups, "sorted", seed=3)
+    dns = bench.slot_groups(S, B, groups, "dense")
+    for gs in (rnd, srt, dns):
+        ids = torch.cat(gs).tolist()
+        assert len(gs) == groups and all(len(g) == B and g.dtype == torch.int32 for g in gs)
+        assert len(set(ids)) == len(ids) and min(ids) >= 1 and max(ids) <= S - 1
+    for a, b in zip(rnd, srt):
+        assert sorted(a.tolist()) == b.tolist()
+    assert any(a.tolist() != b.tolist() for a, b in zip(rnd, srt))
+    assert [g.tolist() for g in dns] == [list(range(1 + i * B, 1 + (i + 1) * B)) for i in range(groups)]
