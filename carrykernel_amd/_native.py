@@ -23,7 +23,7 @@ LIB_PATH = os.path.join(PKG_DIR, "lib", "libcarrykernel_gdn.so")
 # (CK_TIMELINE); loaded only by use_timeline_build()
 TIMELINE_LIB_PATH = os.path.join(PKG_DIR, "lib", "libcarrykernel_gdn_timeline.so")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # enum ck_status
 CK_OK = 0
@@ -57,6 +57,7 @@ _flt = ctypes.c_float
 _SIGNATURES = {
     "ck_last_error": (ctypes.c_char_p, []),
     "ck_abi_version": (_int, []),
+    "ck_set_max_items_per_launch": (_int, [_i64]),
     "ck_gdn_packed_decode": (_int, [
         _vp, _int, _i64,          # mixed_qkv, dtype, stride
         _vp, _int, _i64,          # a
@@ -189,3 +190,11 @@ def dtype_code(t: torch.Tensor, name: str) -> int:
         return DTYPE_CODES[t.dtype]
     except KeyError:
         raise ValueError(f"{name} must be float32, bfloat16 or float16, got {t.dtype}") from None
+
+
+def set_max_items_per_launch(cap: int) -> None:
+    """Lower, process-wide, the work items of one decode launch (0: no lower
+    limit): larger steps then run as consecutive launches over slices of
+    their requests (``ck_set_max_items_per_launch``; used by the tests of the
+    split)."""
+    check(lib().ck_set_max_items_per_launch(int(cap)), "set_max_items_per_launch")

@@ -3,6 +3,8 @@
 // their design are in packed_decode_impl.h.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+#include <cstdlib>
 #include <mutex>
 
 #include "packed_decode_masked.h"
@@ -17,6 +19,27 @@ int launch_masked(const PackedParams& p, int B, int resid_fmt, int per_head, int
   if (p.K <= 64) return launch_masked_k<64>(p, B, resid_fmt, per_head, mode, access, stream);
   if (p.K <= 128) return launch_masked_k<128>(p, B, resid_fmt, per_head, mode, access, stream);
   return launch_masked_k<256>(p, B, resid_fmt, per_head, mode, access, stream);
+}
+
+namespace {
+std::atomic<int64_t> g_max_items{0};
+std::once_flag g_max_items_env;
+
+// CARRYKERNEL_MAX_ITEMS_PER_LAUNCH, read on the first launch (not at every
+// call: getenv can race a setenv of another thread)
+void read_max_items_env() {
+  std::call_once(g_max_items_env, [] {
+    if (const char* e = getenv("CARRYKERNEL_MAX_ITEMS_PER_LAUNCH")) {
+      const long long v = atoll(e);
+      if (v > 0) g_max_items.store(v, std::memory_order_relaxed);
+    }
+  });
+}
+}  // namespace
+
+int64_t max_items_override() {
+  read_max_items_env();
+  return g_max_items.load(std::memory_order_relaxed);
 }
 
 int resident_workgroups(const void* fn, int block, int* per_cu_out) {
@@ -230,7 +253,14 @@ extern "C" int ck_gdn_packed_decode_to(const void* mixed_qkv, int qkv_dtype, int
 
 extern "C" const char* ck_last_error(void) { return ck::last_error().c_str(); }
 
-extern "C" int ck_abi_version(void) { return 1; }
+extern "C" int ck_abi_version(void) { return 2; }
+
+extern "C" int ck_set_max_items_per_launch(int64_t cap) {
+  if (cap < 0) return ck::fail(CK_EINVAL, "the item limit must be >= 0, got %lld", (long long)cap);
+  ck::pd::read_max_items_env();  // so that a later first launch does not overwrite it
+  ck::pd::g_max_items.store(cap, std::memory_order_relaxed);
+  return ck::ok();
+}
 
 #if CK_TIMELINE
 // Timeline build only: device buffer of kTlMaxWorkgroups x kTlSlots uint64

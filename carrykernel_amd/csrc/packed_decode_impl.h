@@ -40,7 +40,6 @@
 
 #include <hip/hip_runtime.h>
 
-#include <cstdlib>
 
 #include "ck_capi_common.h"
 #include "ck_device.h"
@@ -829,16 +828,19 @@ __device__ __forceinline__ void stage_gates(const PackedParams& p, const Geom& g
   if (v * 64 >= n) __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
 }
 
+// A lower limit on the items of one launch set for the process (0: none):
+// CARRYKERNEL_MAX_ITEMS_PER_LAUNCH, read once, or ck_set_max_items_per_launch
+// (packed_decode.hip). Used by the tests of the split.
+int64_t max_items_override();
+
 // Items one launch may hold so that no workgroup gets more than kGateCap:
 // a workgroup's items come from one CU group of ceil(items / m) items, m =
-// resident / per_cu (work_seq; the plain stride gives fewer). A positive
-// CARRYKERNEL_MAX_ITEMS_PER_LAUNCH lowers it (tests of the split).
+// resident / per_cu (work_seq; the plain stride gives fewer), or fewer if the
+// process sets a lower limit (max_items_override).
 inline int64_t launch_item_cap(int resident, int per_cu) {
   int64_t cap = (int64_t)kGateCap * (resident / (per_cu > 1 ? per_cu : 1));
-  if (const char* e = getenv("CARRYKERNEL_MAX_ITEMS_PER_LAUNCH")) {
-    const long long v = atoll(e);
-    if (v > 0 && v < cap) cap = v;
-  }
+  const int64_t v = max_items_override();
+  if (v > 0 && v < cap) cap = v;
   return cap;
 }
 

@@ -80,6 +80,17 @@ const char* ck_last_error(void);
 int ck_abi_version(void);
 
 /*
+ * Lower, for the whole process, the number of work items one decode launch
+ * holds (0: no lower limit, the default): a larger step then runs as
+ * consecutive launches over slices of its requests, as steps past the
+ * built-in limit do. It has no counterpart in the reference: it exists to
+ * test the split. The environment variable CARRYKERNEL_MAX_ITEMS_PER_LAUNCH,
+ * read once at the first launch, sets the same value. Thread-safe; affects
+ * launches issued after it returns.
+ */
+int ck_set_max_items_per_launch(int64_t cap);
+
+/*
  * One decode step of the vLLM-layout quantized GDN, updated in place.
  *
  * mixed_qkv [B, 2*H*K + HV*V] (row stride stride_qkv_tok elements, last dim

@@ -9,8 +9,8 @@ more than one wave) or that the step is split over consecutive launches
   more than 64 items per workgroup; per-row int8 EXACT: 70,400 items, two
   launches) and through the bf16-state arm (two launches): every item is
   checked bit for bit;
-* small steps split into launches of a few items (a lowered
-  CARRYKERNEL_MAX_ITEMS_PER_LAUNCH) with bf16 activations and output,
+* small steps split into launches of a few items (a limit lowered through
+  ck_set_max_items_per_launch) with bf16 activations and output,
   strided ids and out-of-place destinations;
 * C5 at full size (24 layers x B=64 x 2048 tokens, int8 and int6 state,
   mixed alpha), its drift against the fp32 state arm bounded and the
@@ -25,6 +25,7 @@ import torch
 
 import bench
 import oracle
+from carrykernel_amd import _native
 from carrykernel_amd.vllm_integration import quantized_packed_decode as qpd
 from tests._helpers import make_packed_inputs, make_pool
 
@@ -153,8 +154,8 @@ def test_c5_full_size_drift(device, bits, bound):
 
 
 @pytest.mark.parametrize("per_head,resid_fmt,cap", [(True, oracle.RESID_INT4, 40), (False, oracle.RESID_INT8, 150)])
-def test_split_over_launches_small_cap(device, monkeypatch, per_head, resid_fmt, cap):
-    """CARRYKERNEL_MAX_ITEMS_PER_LAUNCH lowers what one launch holds, so a
+def test_split_over_launches_small_cap(device, per_head, resid_fmt, cap):
+    """ck_set_max_items_per_launch lowers what one launch holds, so a
     small step runs as several launches over slices of the requests (the
     per-request pointers advanced on the host): bf16 activations and output,
     strided slot ids, an out-of-place destination, a NULL slot, against the
@@ -171,27 +172,35 @@ def test_split_over_launches_small_cap(device, monkeypatch, per_head, resid_fmt,
     o_ref = oracle.packed_decode(mixed.float().numpy(), a.float().numpy(), b.float().numpy(), A_log.float().numpy(),
                                  dt_bias.float().numpy(), Kl ** -0.5, *ref_pool, src, Hq, use_qk_l2norm=True,
                                  resid_fmt=resid_fmt, per_head=per_head, dst_indices=dst)
-    for split in (True, False):
-        if split:
-            monkeypatch.setenv("CARRYKERNEL_MAX_ITEMS_PER_LAUNCH", str(cap))
-        else:
-            monkeypatch.delenv("CARRYKERNEL_MAX_ITEMS_PER_LAUNCH", raising=False)
-        dpool = [torch.from_numpy(x.copy()).to(device) for x in pool]
-        ids2 = torch.zeros(2 * B, dtype=torch.int32)
-        ids2[::2] = torch.from_numpy(src)
-        ids = ids2.to(device)[::2]
-        out = torch.empty(B, 1, HVl, Vl, dtype=torch.bfloat16, device=device)
-        print(f"case split={split} per_head={per_head} cap={cap}", flush=True)
-        qpd.quantized_gated_delta_rule_packed_decode(
-            mixed.to(device), a.to(device), b.to(device), A_log.to(device), dt_bias.to(device), Kl ** -0.5, *dpool,
-            out, ids, use_qk_l2norm_in_kernel=True, resid_fmt=resid_fmt, dst_state_indices=torch.from_numpy(dst).to(device))
-        torch.cuda.synchronize()
-        np.testing.assert_array_equal(out[:, 0].float().cpu().numpy(), oracle.bf16_round(o_ref), err_msg=f"out split={split}")
-        for name, d, h in zip(("state_codes", "state_scale", "resid_codes", "resid_scale"), dpool, ref_pool):
-            np.testing.assert_array_equal(_host(d), h, err_msg=f"{name} split={split}")
+    try:
+        for split in (True, False):
+            _run_split_case(device, split, cap, per_head, resid_fmt, pool, ref_pool, o_ref, src, dst, mixed, a, b,
+                            A_log, dt_bias, B, Hq, HVl, Kl, Vl)
+    finally:
+        _native.set_max_items_per_launch(0)
 
 
-def test_float_state_split_over_launches_small_cap(device, monkeypatch):
+def _run_split_case(device, split, cap, per_head, resid_fmt, pool, ref_pool, o_ref, src, dst, mixed, a, b, A_log,
+                    dt_bias, B, Hq, HVl, Kl, Vl):
+    """One run of test_split_over_launches_small_cap's step: split into
+    launches of at most `cap` items, or unsplit."""
+    _native.set_max_items_per_launch(cap if split else 0)
+    dpool = [torch.from_numpy(x.copy()).to(device) for x in pool]
+    ids2 = torch.zeros(2 * B, dtype=torch.int32)
+    ids2[::2] = torch.from_numpy(src)
+    ids = ids2.to(device)[::2]
+    out = torch.empty(B, 1, HVl, Vl, dtype=torch.bfloat16, device=device)
+    print(f"case split={split} per_head={per_head} cap={cap}", flush=True)
+    qpd.quantized_gated_delta_rule_packed_decode(
+        mixed.to(device), a.to(device), b.to(device), A_log.to(device), dt_bias.to(device), Kl ** -0.5, *dpool,
+        out, ids, use_qk_l2norm_in_kernel=True, resid_fmt=resid_fmt, dst_state_indices=torch.from_numpy(dst).to(device))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out[:, 0].float().cpu().numpy(), oracle.bf16_round(o_ref), err_msg=f"out split={split}")
+    for name, d, h in zip(("state_codes", "state_scale", "resid_codes", "resid_scale"), dpool, ref_pool):
+        np.testing.assert_array_equal(_host(d), h, err_msg=f"{name} split={split}")
+
+
+def test_float_state_split_over_launches_small_cap(device):
     """The bf16-state arm split into launches of at most 30 items (B=19,
     HV=8, two 64-row items per head), bit for bit against the oracle."""
     B, Hq, HVl, Kl, Vl = 19, 8, 8, 128, 128
@@ -203,11 +212,14 @@ def test_float_state_split_over_launches_small_cap(device, monkeypatch):
     mixed, a, b, A_log, dt_bias = make_packed_inputs(B, Hq, HVl, Kl, Vl, seed=19)
     ids = torch.randperm(S - 1, generator=g)[:B].to(torch.int32) + 1
     out = torch.empty(B, 1, HVl, Vl, device=device)
-    monkeypatch.setenv("CARRYKERNEL_MAX_ITEMS_PER_LAUNCH", "30")
+    _native.set_max_items_per_launch(30)
     print("case float-state split cap=30", flush=True)
-    bench.float_state_step(dstate, mixed.to(device), a.to(device), b.to(device), A_log.to(device),
-                           dt_bias.to(device), Kl ** -0.5, out, ids.to(device), True)
-    torch.cuda.synchronize()
+    try:
+        bench.float_state_step(dstate, mixed.to(device), a.to(device), b.to(device), A_log.to(device),
+                               dt_bias.to(device), Kl ** -0.5, out, ids.to(device), True)
+        torch.cuda.synchronize()
+    finally:
+        _native.set_max_items_per_launch(0)
     o_ref = oracle.packed_decode_float_state(mixed.numpy(), a.numpy(), b.numpy(), A_log.numpy(), dt_bias.numpy(),
                                              Kl ** -0.5, ref_state, ids.numpy(), Hq, bf16=True, use_qk_l2norm=True)
     np.testing.assert_array_equal(_host(out[:, 0]), o_ref)
