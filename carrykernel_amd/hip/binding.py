@@ -69,7 +69,14 @@ class HipModule:
         """Fused GDN + INT8 quantize + error feedback into the caller's
         ``o, h_out, scale_out, e_out, e_scale_out`` (.cu:310-348).
         ``e_scale_in`` / ``e_scale_out`` are read / written for the int8
-        residual only, and always passed, as in the reference."""
+        residual only, and always passed, as in the reference.
+
+        One difference from the CUDA launcher: that kernel loops over any K
+        at run time (.cu:161-166, :185-190), this one takes K in {16, 32,
+        64, 128, 256} (K-slices held in registers, a fixed reduction order
+        per K) and raises ``RuntimeError`` ("K must be ...") for any other
+        K, as the Triton path of statequant/kernel.py:277 (``tl.arange(0,
+        K)``) needs a power of two too."""
         _check_state(h_in, "h_in")
         _check_state(e_in, "e_in")
         _check(h_in.dtype == torch.int8, "h_in must be int8")
@@ -94,7 +101,8 @@ class HipModule:
         _check(st == _native.CK_OK, f"gdn_quant_step: {_last_error(self._lib, st)}")
 
     def gdn_fp32_step(self, h_in, q, k, v, alpha, beta, o, h_out, block_v: int) -> None:
-        """Fused FP32 GDN step into the caller's ``o, h_out`` (.cu:350-371)."""
+        """Fused FP32 GDN step into the caller's ``o, h_out`` (.cu:350-371).
+        K in {16, 32, 64, 128, 256}, as for gdn_quant_step."""
         _check_state(h_in, "h_in")
         _check(h_in.dtype == torch.float32, "h_in must be fp32")
         _check(h_in.dim() == 4, "h_in must be [B, HV, K, V]")

@@ -99,6 +99,10 @@ def test_other_entry_points_argument_errors(L):
     assert rc == _native.CK_EUNSUPPORTED and "K must be" in L.ck_last_error().decode()
     rc = L.ck_gdn_quant_step(p, p, p, p, p, p, p, p, p, p, p, p, p, p, 1, 1, 512, 6, 127.0, 0, 0, None)
     assert rc == _native.CK_EUNSUPPORTED and "K must be" in L.ck_last_error().decode()
+    # unlike the CUDA launcher (any K), the statequant step takes K in {16 .. 256}, powers of two
+    for k_bad in (48, 96, 100):
+        rc = L.ck_gdn_quant_step(p, p, p, p, p, p, p, p, p, p, p, p, p, p, 1, 1, k_bad, 6, 127.0, 0, 0, None)
+        assert rc == _native.CK_EUNSUPPORTED and "K must be" in L.ck_last_error().decode()
     odd = ctypes.c_void_p(17)   # an fp16 residual at an odd address
     rc = L.ck_gdn_quant_step(p, p, odd, p, p, p, p, p, p, p, p, p, p, p, 1, 1, 32, 6, 127.0, 1, 0, None)
     assert rc == _native.CK_EINVAL and "2-byte aligned" in L.ck_last_error().decode()
