@@ -20,7 +20,9 @@ do when 24 layers share the cache between two steps of one layer.
 
 Prints ONE JSON line (rank 0). ``value`` is algorithmic GB/s over the timed
 steps; ``ms_per_step`` is the device time per step from HIP events on the
-launch stream.
+launch stream. The headline times exactly --steps after exactly --warmup
+steps; each ``sweep`` line records the steps and warm-up it timed, at least
+those and at least 1 ms / 0.4 ms of work (``sweep_window``).
 """
 
 from __future__ import annotations
@@ -43,6 +45,12 @@ from carrykernel_amd.statequant import kernel as sq  # noqa: E402
 from carrykernel_amd.vllm_integration import quantized_packed_decode as qpd  # noqa: E402
 
 HBM_PEAK_GBPS = 8000.0
+# Sweep lines (not the headline) time a window of at least SWEEP_WINDOW_US of
+# device work after at least SWEEP_WARM_US of warm-up steps: each follows the
+# CPU leg's check of that line, which leaves the GPU idle, and a 20-step window
+# of a 6 us step then reads the clocks' ramp rather than the step.
+SWEEP_WINDOW_US = 1000.0
+SWEEP_WARM_US = 400.0
 METRIC = "\u00b5s per GDN decode step and achieved HBM GB/s (% roofline) at batch 64, 1 GPU"
 H = HV = 32
 K = V = 128
@@ -440,6 +448,15 @@ def slot_groups(S, B, groups, order, seed=0):
     if order == "sorted":
         out = [torch.sort(g).values for g in out]
     return [g.to(torch.int32) for g in out]
+
+
+def sweep_window(nbytes, steps, warmup):
+    """(steps, warmup) for a sweep line moving `nbytes` per step: at least the
+    driver's K and W, and enough steps, at a step time estimated from the
+    bytes at 5 TB/s (5 us at least), for SWEEP_WINDOW_US of timed and
+    SWEEP_WARM_US of warm-up work."""
+    est_us = max(5.0, nbytes / 5.0e6)
+    return max(steps, math.ceil(SWEEP_WINDOW_US / est_us)), max(warmup, math.ceil(SWEEP_WARM_US / est_us))
 
 
 def run_config(device, B, resid_fmt, per_head, steps, warmup, groups, quant_mode="fast", seed=0,
@@ -1121,27 +1138,29 @@ def main():
     if args.batch == 64 and args.resid == "int4" and args.rscale == "head":
         sweep[key(64, "int4_head", args.quant_mode)] = {
             "us": line["us_per_step"], "host_us": line["host_us_per_eager_call"], "GBps": line["value"],
-            "frac": line["roofline"]["frac"], "validated": r["validated"]}
+            "frac": line["roofline"]["frac"], "steps": args.steps, "warmup": args.warmup,
+            "validated": r["validated"]}
     for bb, fmt_name, mode in cases:
         if key(bb, fmt_name, mode) in sweep:
             continue
         fmt, ph = formats[fmt_name]
         groups = max(2, min(64, 1024 // bb))
-        rr = run_config(device, bb, fmt, ph, args.steps, args.warmup, groups, mode, cpu=cpu,
-                        name=key(bb, fmt_name, mode))
         nb = algorithmic_bytes(bb, H, HV, K, V, fmt, ph)
+        st, wu = sweep_window(nb, args.steps, args.warmup)
+        rr = run_config(device, bb, fmt, ph, st, wu, groups, mode, cpu=cpu, name=key(bb, fmt_name, mode))
         sweep[key(bb, fmt_name, mode)] = {"us": round(rr["ms"] * 1e3, 3), "host_us": round(rr["host_ms"] * 1e3, 3),
                                           "GBps": round(nb / (rr["ms"] * 1e-3) / 1e9, 1),
                                           "frac": round(nb / (rr["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-                                          "validated": rr["validated"]}
+                                          "steps": st, "warmup": wu, "validated": rr["validated"]}
     if not args.no_sweep:   # the headline step with vLLM's bf16 activations and output
-        rr = run_config(device, 64, qpd.RESID_INT4, True, args.steps, args.warmup, 16, args.quant_mode,
-                        act_dtype=torch.bfloat16, cpu=cpu, name="B64_int4_head_bf16act")
         nb = algorithmic_bytes(64, H, HV, K, V, qpd.RESID_INT4, True, act_bytes=2)
+        st, wu = sweep_window(nb, args.steps, args.warmup)
+        rr = run_config(device, 64, qpd.RESID_INT4, True, st, wu, 16, args.quant_mode,
+                        act_dtype=torch.bfloat16, cpu=cpu, name="B64_int4_head_bf16act")
         sweep["B64_int4_head_bf16act"] = {"us": round(rr["ms"] * 1e3, 3), "host_us": round(rr["host_ms"] * 1e3, 3),
                                           "GBps": round(nb / (rr["ms"] * 1e-3) / 1e9, 1),
                                           "frac": round(nb / (rr["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-                                          "validated": rr["validated"]}
+                                          "steps": st, "warmup": wu, "validated": rr["validated"]}
     if not args.no_sweep:
         # the C5 shape through 24 layers per token: eager vs one graph per token,
         # full and NULL-padded (48 live requests in a batch-64 capture)

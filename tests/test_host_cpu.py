@@ -445,3 +445,15 @@ def test_bench_slot_groups_orders():
         assert sorted(a.tolist()) == b.tolist()
     assert any(a.tolist() != b.tolist() for a, b in zip(rnd, srt))
     assert [g.tolist() for g in dns] == [list(range(1 + i * B, 1 + (i + 1) * B)) for i in range(groups)]
+
+
+def test_bench_sweep_window():
+    """bench.sweep_window: never fewer than the driver's K / W; small steps
+    get enough steps for 1 ms of timed and 0.4 ms of warm-up work at the
+    5 us floor; a step estimated above 1 ms keeps K and W."""
+    import bench
+    assert bench.sweep_window(1, 20, 5) == (200, 80)              # 5 us floor
+    nb64 = bench.algorithmic_bytes(64, 32, 32, 128, 128, qpd.RESID_INT4, True)
+    assert bench.sweep_window(nb64, 20, 5) == (47, 19)            # ~21.4 us at 5 TB/s
+    assert bench.sweep_window(nb64, 100, 50) == (100, 50)
+    assert bench.sweep_window(10 * 5.0e9, 20, 5) == (20, 5)       # 10 ms estimate
