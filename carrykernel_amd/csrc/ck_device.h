@@ -154,8 +154,10 @@ __device__ __forceinline__ void load_act16(const void* p, int64_t i, int dtype, 
 }
 
 // ---------------------------------------------------------------------------
-// Cross-lane reductions over aligned groups of N lanes (N = 1, 2, 4, 8, 16),
-// built from DPP moves. Each step adds the value of a partner lane; because
+// Cross-lane reductions over aligned groups of N lanes (N = 1, 2, 4, 8, 16,
+// 32, 64), built from DPP moves within a row of 16 lanes and ds_swizzle /
+// ds_bpermute lane exchanges (__shfl_xor) across rows. Each step adds the
+// value of a partner lane; because
 // fp32 addition is commutative both partners obtain the same bits, so the
 // result is the balanced tree ((p0+p1)+(p2+p3)) + ((p4+p5)+(p6+p7)) ... in
 // every lane of the group, independent of which lane is "self".
@@ -172,11 +174,13 @@ __device__ __forceinline__ float dpp_f(float x) {
 
 template <int N>
 __device__ __forceinline__ float group_sum(float x) {
-  static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16, "group size");
+  static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16 || N == 32 || N == 64, "group size");
   if constexpr (N >= 2) x = x + dpp_f<kDppQuadXor1>(x);
   if constexpr (N >= 4) x = x + dpp_f<kDppQuadXor2>(x);
   if constexpr (N >= 8) x = x + dpp_f<kDppRowHalfMirror>(x);
   if constexpr (N >= 16) x = x + dpp_f<kDppRowMirror>(x);
+  if constexpr (N >= 32) x = x + __shfl_xor(x, 16);
+  if constexpr (N >= 64) x = x + __shfl_xor(x, 32);
   return x;
 }
 
@@ -191,12 +195,14 @@ __device__ __forceinline__ uint32_t dpp_u(uint32_t x) {
 
 template <int N>
 __device__ __forceinline__ float group_max(float x) {
-  static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16, "group size");
+  static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16 || N == 32 || N == 64, "group size");
   uint32_t u = __float_as_uint(x);
   if constexpr (N >= 2) u = max(u, dpp_u<kDppQuadXor1>(u));
   if constexpr (N >= 4) u = max(u, dpp_u<kDppQuadXor2>(u));
   if constexpr (N >= 8) u = max(u, dpp_u<kDppRowHalfMirror>(u));
   if constexpr (N >= 16) u = max(u, dpp_u<kDppRowMirror>(u));
+  if constexpr (N >= 32) u = max(u, (uint32_t)__shfl_xor((int)u, 16));
+  if constexpr (N >= 64) u = max(u, (uint32_t)__shfl_xor((int)u, 32));
   return __uint_as_float(u);
 }
 

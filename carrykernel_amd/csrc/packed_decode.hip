@@ -18,7 +18,9 @@ int launch_masked(const PackedParams& p, int B, int resid_fmt, int per_head, int
   if (p.K <= 32) return launch_masked_k<32>(p, B, resid_fmt, per_head, mode, access, stream);
   if (p.K <= 64) return launch_masked_k<64>(p, B, resid_fmt, per_head, mode, access, stream);
   if (p.K <= 128) return launch_masked_k<128>(p, B, resid_fmt, per_head, mode, access, stream);
-  return launch_masked_k<256>(p, B, resid_fmt, per_head, mode, access, stream);
+  if (p.K <= 256) return launch_masked_k<256>(p, B, resid_fmt, per_head, mode, access, stream);
+  if (p.K <= 512) return launch_masked_k<512>(p, B, resid_fmt, per_head, mode, access, stream);
+  return launch_masked_k<1024>(p, B, resid_fmt, per_head, mode, access, stream);
 }
 
 namespace {
@@ -113,7 +115,7 @@ static int packed_decode_impl(const void* mixed_qkv, int qkv_dtype, int64_t stri
     return fail(CK_EINVAL, "quant_mode must be CK_QUANT_FAST or CK_QUANT_EXACT, got %d", quant_mode);
   if (state_bits < 2 || state_bits > 8) return fail(CK_EINVAL, "state_bits must be in 2..8, got %d", state_bits);
   if (num_slots <= 0) return fail(CK_EINVAL, "num_slots must be positive");
-  if (K > 256) return fail(CK_EUNSUPPORTED, "K must be at most 256, got %d", K);
+  if (K > 1024) return fail(CK_EUNSUPPORTED, "K must be at most 1024, got %d", K);
   if (resid_fmt == CK_RESID_INT4 && K % 2 != 0)
     return fail(CK_EINVAL, "int4 residual packing needs an even K, got %d", K);
   if (B == 0) return ok();

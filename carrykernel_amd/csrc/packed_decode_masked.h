@@ -1,4 +1,4 @@
-// Fused decode for any pool row length K in 1 .. 256 and any row alignment:
+// Fused decode for any pool row length K in 1 .. 1024 and any row alignment:
 // the reference masks its K lanes with o_k < K and loads zeros past K
 // (vllm_integration/quantized_packed_decode.py:123-127, :158, :165-166,
 // :196-202; BK = next_pow2(K) at :303), so a row of
@@ -186,7 +186,14 @@ int launch_masked_shape(const PackedParams& p, int B, hipStream_t s) {
     if (p.V <= RPI * 4 * 2) return launch_masked_cfg<KP, 4, 2, RESID, true, MODE, DST, MASK>(p, B, s);
     if (p.V <= RPI * 4 * 4) return launch_masked_cfg<KP, 4, 4, RESID, true, MODE, DST, MASK>(p, B, s);
     if (p.V <= RPI * 4 * 8) return launch_masked_cfg<KP, 4, 8, RESID, true, MODE, DST, MASK>(p, B, s);
-    return fail(CK_EUNSUPPORTED, "per-head residual scale supports V <= %d at K=%d, got V=%d", RPI * 32, p.K, p.V);
+    // rows of 512 or 1024 codes: 2 or 1 rows per wave instruction, so a head
+    // of V = 128 or 64 rows takes 16 waves of 4 rows per lane
+    constexpr int kMaxWaves = KP >= 512 ? 16 : 8;
+    if constexpr (KP >= 512) {
+      if (p.V <= RPI * 4 * 16) return launch_masked_cfg<KP, 4, 16, RESID, true, MODE, DST, MASK>(p, B, s);
+    }
+    return fail(CK_EUNSUPPORTED, "per-head residual scale supports V <= %d at K=%d, got V=%d", RPI * 4 * kMaxWaves,
+                p.K, p.V);
   }
 }
 

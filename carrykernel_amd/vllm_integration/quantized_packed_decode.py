@@ -56,9 +56,11 @@ RESID_INT4 = 1
 HAS_HIP = _native.library_available()
 
 # The reference takes any K (its BK = next_pow2(K) lanes are masked past K);
-# here K up to 256. Power-of-two K from 16 with 16-byte aligned pool rows run
-# the bandwidth kernel, every other K or row alignment the masked kernel.
-MAX_K = 256
+# here K up to 1024. Power-of-two K from 16 to 256 with 16-byte aligned pool
+# rows run the bandwidth kernel, every other K or row alignment the masked
+# kernel (rows padded to 512 or 1024 lanes above 256; a per-head residual
+# scale there needs V <= 128 at K <= 512 and V <= 64 above).
+MAX_K = 1024
 
 _QUANT_MODES = {"fast": _native.QUANT_FAST, "exact": _native.QUANT_EXACT}
 

@@ -47,7 +47,7 @@ extern "C" {
 enum ck_status {
   CK_OK = 0,
   CK_EINVAL = 1,       /* bad argument (null pointer, bad size/stride/dtype)   */
-  CK_EUNSUPPORTED = 2, /* valid but not implemented here (e.g. K not in 16..256) */
+  CK_EUNSUPPORTED = 2, /* valid but not implemented here (e.g. K above 1024) */
   CK_ELAUNCH = 3       /* the HIP runtime rejected the kernel launch            */
 };
 
@@ -107,7 +107,8 @@ int ck_set_max_items_per_launch(int64_t cap);
  *   block (out gets zeros, state untouched); slot >= num_slots is out of range
  *   (out gets NaN, state untouched).
  * state_bits: the state code range is +-(2^(state_bits-1) - 1), bits in 2..8.
- * Requirements: K in 1..256 (even for CK_RESID_INT4); HV % H == 0. Rows of
+ * Requirements: K in 1..1024 (even for CK_RESID_INT4); HV % H == 0; with
+ *   CK_RSCALE_PER_HEAD above K = 256, V <= 128 (K <= 512) or V <= 64. Rows of
  *   K = 16, 32, 64, 128 or 256 codes, 16-byte aligned (8-byte for int4
  *   residual rows), run the bandwidth kernel; any other K or alignment runs
  *   the masked kernel, which computes as if every row, q and k were

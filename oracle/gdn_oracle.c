@@ -141,9 +141,10 @@ static float tree_sum(float* c, int n) {
   return c[0];
 }
 
-/* sum_k x[k*sx] * y[k*sy] over K (K a multiple of 16, K/16 a power of 2). */
+/* sum_k x[k*sx] * y[k*sy] over K (K a multiple of 16, K/16 a power of 2,
+   K <= 1024). */
 static float dot_k(const float* x, int64_t sx, const float* y, int64_t sy, int K) {
-  float chunk[16];
+  float chunk[64];
   const int nc = K / 16;
   for (int cidx = 0; cidx < nc; ++cidx) {
     const float* xc = x + (int64_t)cidx * 16 * sx;
@@ -210,12 +211,12 @@ int orc_packed_decode(const float* mixed, int64_t stride_mixed,
                       int l2norm, int resid_fmt, int per_head, int state_bits, int mode, int nthreads) {
   /* dst_idx (may be NULL: in place): the updated state of request n goes to
      slot dst_idx[n]; one outside [1, num_slots) discards it (out is kept).
-     Any K in 1..256 (even for the int4 residual): the reference's lanes
+     Any K in 1..1024 (even for the int4 residual): the reference's lanes
      o_k < BK = next_pow2(K) load 0 past K (qpd:123-127, :158, :165-166,
      :196-202, :303), so the step runs on rows zero-padded to
      KP = max(16, next_pow2(K)) in the reduction order of KP and stores the
      K existing columns. */
-  if (K < 1 || K > 256 || HV % H != 0 || (resid_fmt == 1 && K % 2 != 0)) return 1;
+  if (K < 1 || K > 1024 || HV % H != 0 || (resid_fmt == 1 && K % 2 != 0)) return 1;
   int KP = 16;
   while (KP < K) KP *= 2;
   const float qmax = (float)((1 << (state_bits - 1)) - 1);

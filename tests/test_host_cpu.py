@@ -55,7 +55,10 @@ def _pd_args(**over):
 
 
 @pytest.mark.parametrize("over,status,msg", [
-    (dict(K=300), _native.CK_EUNSUPPORTED, "K must be at most 256"),
+    (dict(K=1030), _native.CK_EUNSUPPORTED, "K must be at most 1024"),
+    # a per-head residual scale keeps a whole head in one workgroup: 64 rows of 1024 codes at most
+    (dict(K=1024, V=128, stride_state=2 * 128 * 1024, stride_sscale=256, stride_resid=2 * 128 * 512),
+     _native.CK_EUNSUPPORTED, "per-head residual scale supports V <= 64 at K=1024, got V=128"),
     (dict(K=25), _native.CK_EINVAL, "even K"),
     (dict(HV=3, H=2), _native.CK_EINVAL, "multiple of H"),
     (dict(qkv_dtype=7), _native.CK_EINVAL, "dtype"),
@@ -169,13 +172,13 @@ def test_qpd_value_errors(mutate, msg):
 
 
 def test_qpd_k_limits():
-    """K above 256 is refused; an odd K cannot hold an int4 residual (two
+    """K above 1024 is refused; an odd K cannot hold an int4 residual (two
     codes per byte: the reference's packing check, quantized_packed_decode.py:
     278-281, fires before its even-K check at :306-307, which the C ABI keeps);
     any other K is accepted and, on CPU tensors, stops at the missing GPU (no
     host path)."""
-    c = _cpu_case(K=264, resid_fmt=qpd.RESID_INT8)
-    with pytest.raises(ValueError, match="packed decode supports K <= 256"):
+    c = _cpu_case(K=1040, resid_fmt=qpd.RESID_INT8)
+    with pytest.raises(ValueError, match="packed decode supports K <= 1024"):
         qpd.quantized_gated_delta_rule_packed_decode(**c)
     c = _cpu_case(K=24, resid_fmt=qpd.RESID_INT4)
     c.update(mixed_qkv=torch.zeros(2, 2 * 2 * 25 + 4 * 32),
@@ -183,7 +186,8 @@ def test_qpd_k_limits():
              resid_codes=torch.zeros(3, 4, 32, 12, dtype=torch.int8))
     with pytest.raises(ValueError, match="packed two codes per byte"):
         qpd.quantized_gated_delta_rule_packed_decode(**c)
-    for K, fmt in ((48, qpd.RESID_INT8), (7, qpd.RESID_INT8), (100, qpd.RESID_INT4)):
+    for K, fmt in ((48, qpd.RESID_INT8), (7, qpd.RESID_INT8), (100, qpd.RESID_INT4), (264, qpd.RESID_INT8),
+                   (1024, qpd.RESID_INT4)):
         with pytest.raises(_native.HipUnavailable):
             qpd.quantized_gated_delta_rule_packed_decode(**_cpu_case(K=K, resid_fmt=fmt))
 

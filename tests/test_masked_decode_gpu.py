@@ -1,5 +1,5 @@
 """GPU parity of the any-K decode path (packed_decode_masked.h): pool rows
-whose K is not a power of two from 16 (K = 2 ... 240: byte-granular
+whose K is not a power of two from 16 to 256 (K = 1 ... 1024: byte-granular
 accesses, 4-byte state and 2- or 4-byte residual accesses when K is a
 multiple of 4, or whole 16-byte lanes when K is a multiple of 16), and
 power-of-two K whose pool rows are not aligned for the bandwidth kernel's
@@ -63,6 +63,21 @@ CASES = {
                                       2, True),
     "k256_misaligned_int4_row_out_of_place": (256, 4, 1, 2, 64, I4, False, "fast", F32, F32, True, 0.0, False,
                                               True, 8, 2, True),
+    # K above 256: rows padded to 512 lanes (32 lanes per row) or 1024 (a whole wave per row)
+    "k384_int8_row_lanes": (384, 4, 2, 4, 64, I8, False, "fast", F32, F32, True, 0.1, True, False, 8, 2, False),
+    "k512_int4_head_lanes_v128": (512, 3, 1, 2, 128, I4, True, "fast", F32, F32, True, 0.0, False, False, 8, 2,
+                                  False),
+    "k300_int4_row_words_exact": (300, 4, 2, 4, 50, I4, False, "exact", BF16, F32, True, 0.0, False, False, 8, 2,
+                                  False),
+    "k333_int8_head_bytes_exact": (333, 3, 1, 2, 20, I8, True, "exact", F32, F32, True, 0.0, False, False, 8, 2,
+                                   False),
+    "k1000_int8_head_words_gqa": (1000, 3, 1, 3, 64, I8, True, "fast", F32, F32, True, 0.0, True, False, 8, 2,
+                                  False),
+    # 16 x 4 x 32 = 2048 tiles of 4 rows: the one-wave, 4-rows-per-lane shape at 1024 lanes
+    "k1024_int4_row_lanes_many_tiles_exact": (1024, 16, 2, 4, 128, I4, False, "exact", F16, F16, True, 0.1, False,
+                                              False, 8, 2, False),
+    "k520_misaligned_int4_row_out_of_place": (520, 4, 1, 2, 40, I4, False, "fast", F32, F32, True, 0.0, False, True,
+                                              8, 2, True),
 }
 
 

@@ -146,7 +146,9 @@ def test_packed_decode_matches_bruteforce(resid_fmt, per_head, exact, l2norm, bi
 
 @pytest.mark.parametrize("K,resid_fmt,exact", [(7, oracle.RESID_INT8, False), (24, oracle.RESID_INT4, True),
                                                (24, oracle.RESID_INT8, False), (2, oracle.RESID_INT4, False),
-                                               (100, oracle.RESID_INT8, True), (200, oracle.RESID_INT4, False)])
+                                               (100, oracle.RESID_INT8, True), (200, oracle.RESID_INT4, False),
+                                               (300, oracle.RESID_INT8, True), (512, oracle.RESID_INT4, False),
+                                               (1000, oracle.RESID_INT4, True)])
 @pytest.mark.parametrize("per_head", [False, True])
 def test_packed_decode_any_k_matches_bruteforce(K, resid_fmt, exact, per_head):
     """K that is not a power of two from 16: the brute force pads q, k and
