@@ -941,6 +941,52 @@ void packed_decode_kernel(const int32_t* __restrict__ idx, int items, int stride
   }
 }
 
+// A launch with no more items than resident workgroups: one item per
+// workgroup, its loads, the gates, the item, with no prefetch of a next item.
+// The persistent kernel's loop would issue a past-the-end prefetch before the
+// item and, at the joins of its conditional stores, wait for some of those
+// loads; this kernel has no younger loads to wait for (graph-replayed, int4,
+// HV=32, us: per head B=1 5.70 -> 5.13, B=8 6.89 -> 6.36; per row B=1 4.53 ->
+// 4.01; the same code computes the item, so the results are the same bits).
+template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ACT, bool DST>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(kMinWavesPerEU<RPL, WAVES>)))
+void packed_decode_single_kernel(const int32_t* __restrict__ idx, int items, int stride_idx, uint32_t nvt_d,
+                                 uint32_t nvt_m, uint32_t nvt_sh, uint32_t hv_d, uint32_t hv_m, uint32_t hv_sh,
+                                 int share_n, uint32_t shares, int grid, const PackedParams p,
+                                 const int32_t* __restrict__ dst_idx) {
+  using L = Layout<K, RPL, WAVES, RESID, PER_HEAD>;
+  const Geom gm{items, stride_idx, share_n, shares, FastDiv{nvt_d, nvt_m, nvt_sh}, FastDiv{hv_d, hv_m, hv_sh}, grid};
+  __shared__ __attribute__((aligned(16))) float s_qk[4][2 * K];  // [0] staged, [2] raw
+  __shared__ float s_red[2][WAVES];
+  __shared__ float4 s_ek[kResidInLds<RPL, RESID, PER_HEAD> ? WAVES * RPL * 4 * 64 : 1];
+  __shared__ float2 s_gate[1];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c = lane % L::LPR;
+  const int g = lane / L::LPR;
+  tl_start(p);
+  const int item = (int)blockIdx.x;
+  const ItemCoord ca = item_coord<false, DST>(p, gm, idx, dst_idx, item);
+#if CK_TIMELINE
+  asm volatile("" ::"s"((int)ca.slot));
+  tl_mark(p, 32);
+#endif
+  const int row0 = ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g;
+  ItemRegs<RPL, L::EW, L::QKT> A;
+  load_item<K, RPL, WAVES, RESID, PER_HEAD, ACT>(p, ca, true, row0, c, A);
+  tl_mark(p, 33);
+  stage_gates<1, false>(p, gm, WorkSeq{item, 1, 1}, wave, lane, s_gate);  // wave 0: this item's gates
+  tl_mark(p, 34);
+  __syncthreads();
+  const float2 gab = s_gate[0];
+  tl_mark(p, tl_item_slot(0, 0));
+  tl_data_ready(p, 0, A);
+  process_item<K, RPL, WAVES, RESID, PER_HEAD, MODE, ACT, DST>(p, ca, row0, c, lane, wave, 0, gab.x, gab.y, A, s_qk,
+                                                              s_red, s_ek);
+  tl_mark(p, tl_item_slot(0, 2));
+}
+
 // Resident workgroups per GPU for a kernel (occupancy x CUs), cached per
 // device; *per_cu (if given) receives the occupancy per CU.
 int resident_workgroups(const void* fn, int block, int* per_cu = nullptr);
@@ -973,6 +1019,13 @@ int launch_cfg(PackedParams p, int B, hipStream_t stream) {
   }
   // fewest items per workgroup, then the fewest workgroups achieving it
   const int per_wg = (p.items + resident - 1) / resident;
+  if (per_wg == 1) {
+    hipLaunchKernelGGL((packed_decode_single_kernel<K, RPL, WAVES, RESID, PER_HEAD, MODE, ACT, DST>),
+                       dim3((unsigned)p.items), dim3(WAVES * 64), 0, stream, p.idx, p.items, p.stride_idx,
+                       p.div_nvt.d, p.div_nvt.m, p.div_nvt.sh, p.div_hv.d, p.div_hv.m, p.div_hv.sh, 0, 0u, p.items,
+                       p, p.dst_idx);
+    return check_launch("ck_gdn_packed_decode");
+  }
   const int grid = (p.items + per_wg - 1) / per_wg;
   set_cu_shares(p, grid, resident, per_cu);
   hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(WAVES * 64), 0, stream, p.idx, p.items, p.stride_idx, p.div_nvt.d,

@@ -22,15 +22,16 @@ pytestmark = pytest.mark.gpu
 DTYPES = (torch.float32, torch.bfloat16, torch.float16)
 
 
-def _draw(seed, any_k=False):
-    """A random decode configuration. any_k: K anywhere in 1..256 (even with
-    the int4 residual), the masked kernel's shapes."""
+def _draw(seed, any_k=False, k_max=256):
+    """A random decode configuration. any_k: K anywhere in 1..k_max (even with
+    the int4 residual; 257..k_max when k_max > 256), the masked kernel's
+    shapes."""
     rng = np.random.default_rng(seed)
     if any_k:
         resid_fmt = int(rng.choice([qpd.RESID_INT8, qpd.RESID_INT4]))
-        K = int(rng.integers(1, 257))
+        K = int(rng.integers(1 if k_max <= 256 else 257, k_max + 1))
         if resid_fmt == qpd.RESID_INT4 and K % 2:
-            K += 1 if K < 256 else -1
+            K += 1 if K < k_max else -1
     else:
         K = int(rng.choice([16, 32, 64, 128, 256]))
     KP = 16
@@ -38,7 +39,9 @@ def _draw(seed, any_k=False):
         KP *= 2
     per_head = bool(rng.integers(2))
     rows_per_inst = 64 // (KP // 16)
-    v_max = rows_per_inst * 32 if per_head else 300      # the per-head shapes hold the head in one workgroup
+    # the per-head shapes hold the head in one workgroup: 32 rows per lane-row
+    # group up to KP = 256 (8 waves x 4 rows), 64 from 512 (16 waves x 4 rows)
+    v_max = rows_per_inst * (64 if KP >= 512 else 32) if per_head else 300
     V = int(rng.integers(1, min(v_max, 300) + 1))
     H = int(rng.choice([1, 2, 4]))
     HV = H * int(rng.choice([1, 2, 3]))
@@ -71,6 +74,12 @@ def test_random_any_k_configuration_bit_exact(device, seed):
     """K drawn from 1..256: the masked kernel (and, when the draw is a power
     of two from 16, the bandwidth kernel)."""
     _run_decode(device, seed, _draw(7000 + seed, any_k=True))
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_large_k_configuration_bit_exact(device, seed):
+    """K drawn from 257..1024: rows padded to 512 or 1024 lanes."""
+    _run_decode(device, seed, _draw(7500 + seed, any_k=True, k_max=1024))
 
 
 def _run_decode(device, seed, c):
