@@ -16,6 +16,13 @@
 // such exchanges per step (h.k, h.q, amax, and the int8 residual's amax), one
 // barrier each.
 //
+// Any K in 1..256: the reference's CUDA launcher loops over its K rows
+// (cuda/gdn_state_kernel.cu:141-246) and the Triton kernel masks its BK =
+// next_pow2(K) rows (statequant/kernel.py:277-279). Here the rows are padded
+// with zeros to KP = max(16, next_pow2(K)) and the KP kernel runs on them (MK:
+// rows at or past K load nothing, contribute zero products and zero to every
+// amax, and store nothing), so the sums keep the KP slice order.
+//
 // Columns per thread. CPT = 4 when V % 4 == 0 and every tensor is 16-byte
 // aligned: a thread's columns are one vector access per row (a dword of
 // codes), so each half-wave reads 128 contiguous bytes of a row. Otherwise
@@ -178,10 +185,11 @@ struct StepParams {
   void* e_out;
   float* e_scale_out;
   int HV, V, nvt;
+  int K;  // rows that exist (the kernel's K template argument is the padded count)
   float qmax, rqmax;
 };
 
-template <int K, int RES, int MODE, int CPT>
+template <int K, int RES, int MODE, int CPT, bool MK>
 __global__ __launch_bounds__(kThreadsFor<K>) void quant_step_kernel(const StepParams p) {
   constexpr int S = kSlicesFor<K>;
   constexpr int RPS = K / S;            // rows per slice
@@ -197,7 +205,8 @@ __global__ __launch_bounds__(kThreadsFor<K>) void quant_step_kernel(const StepPa
   const int c0 = vt * NC + lc;
   const bool colok = c0 < p.V;       // CPT = 4 only with V % 4 == 0: all 4 columns or none
   const int r0 = ks * RPS;
-  const int64_t mb = (int64_t)w * K * p.V;
+  const int KA = MK ? p.K : K;       // rows that exist
+  const int64_t mb = (int64_t)w * KA * p.V;
   const int64_t vb = (int64_t)w * p.V;
   const float alpha = p.alpha[w];
   const float beta = p.beta[w];
@@ -213,8 +222,11 @@ __global__ __launch_bounds__(kThreadsFor<K>) void quant_step_kernel(const StepPa
   float kk[RPS], qq[RPS];
 #pragma unroll
   for (int r = 0; r < RPS; ++r) {
-    kk[r] = p.k[(int64_t)w * K + r0 + r];
-    qq[r] = p.q[(int64_t)w * K + r0 + r];
+    kk[r] = qq[r] = 0.f;
+    if (!MK || r0 + r < KA) {
+      kk[r] = p.k[(int64_t)w * KA + r0 + r];
+      qq[r] = p.q[(int64_t)w * KA + r0 + r];
+    }
   }
   if (colok) {
     ld_f32<CPT>(p.scale_in + vb + c0, sc);
@@ -222,6 +234,12 @@ __global__ __launch_bounds__(kThreadsFor<K>) void quant_step_kernel(const StepPa
     if constexpr (RES == kResInt8) ld_f32<CPT>(p.e_scale_in + vb + c0, esc);
 #pragma unroll
     for (int r = 0; r < RPS; ++r) {
+      if (MK && r0 + r >= KA) {  // padding row: zero codes and residual (decodes to +0 in every format)
+        cw[r] = 0;
+#pragma unroll
+        for (int j = 0; j < EWD; ++j) ew[r][j] = 0u;
+        continue;
+      }
       const int64_t i = mb + (int64_t)(r0 + r) * p.V + c0;
       cw[r] = ld_b8<CPT>(p.h_in + i);
       if constexpr (RES == kResFp32) {
@@ -333,7 +351,7 @@ __global__ __launch_bounds__(kThreadsFor<K>) void quant_step_kernel(const StepPa
       h[r][j] = residual<MODE>(h[r][j], code, s[j]);
       ea[j] = fmaxf(ea[j], fabsf(h[r][j]));
     }
-    if (colok) st_b8<CPT>(p.h_out + mb + (int64_t)(r0 + r) * p.V + c0, pack_codes<CPT>(yb));
+    if (colok && (!MK || r0 + r < KA)) st_b8<CPT>(p.h_out + mb + (int64_t)(r0 + r) * p.V + c0, pack_codes<CPT>(yb));
   }
   if (ks == 0 && colok) st_f32<CPT>(p.scale_out + vb + c0, s);
 
@@ -350,6 +368,7 @@ __global__ __launch_bounds__(kThreadsFor<K>) void quant_step_kernel(const StepPa
     if (colok) {
 #pragma unroll
       for (int r = 0; r < RPS; ++r) {
+        if (MK && r0 + r >= KA) continue;
         uint32_t eb[CPT];
 #pragma unroll
         for (int j = 0; j < CPT; ++j) (void)quantize<MODE>(h[r][j], es[j], inv_e[j], eb[j]);
@@ -360,6 +379,7 @@ __global__ __launch_bounds__(kThreadsFor<K>) void quant_step_kernel(const StepPa
   } else if (colok) {
 #pragma unroll
     for (int r = 0; r < RPS; ++r) {
+      if (MK && r0 + r >= KA) continue;
       const int64_t i = mb + (int64_t)(r0 + r) * p.V + c0;
       if constexpr (RES == kResFp32) {
         st_f32<CPT>(static_cast<float*>(p.e_out) + i, h[r]);
@@ -386,9 +406,10 @@ struct Fp32Params {
   float* o;
   float* h_out;
   int V, nvt;
+  int K;  // rows that exist (the kernel's K template argument is the padded count)
 };
 
-template <int K, int CPT>
+template <int K, int CPT, bool MK>
 __global__ __launch_bounds__(kThreadsFor<K>) void fp32_step_kernel(const Fp32Params p) {
   constexpr int S = kSlicesFor<K>;
   constexpr int RPS = K / S;
@@ -403,19 +424,24 @@ __global__ __launch_bounds__(kThreadsFor<K>) void fp32_step_kernel(const Fp32Par
   const int c0 = vt * NC + lc;
   const bool colok = c0 < p.V;
   const int r0 = ks * RPS;
-  const int64_t mb = (int64_t)w * K * p.V;
+  const int KA = MK ? p.K : K;  // rows that exist
+  const int64_t mb = (int64_t)w * KA * p.V;
   const int64_t vb = (int64_t)w * p.V;
   const float alpha = p.alpha[w];
   const float beta = p.beta[w];
   float h[RPS][CPT], kk[RPS], qq[RPS], vv[CPT];
 #pragma unroll
   for (int r = 0; r < RPS; ++r) {
-    kk[r] = p.k[(int64_t)w * K + r0 + r];
-    qq[r] = p.q[(int64_t)w * K + r0 + r];
+    const bool rin = !MK || r0 + r < KA;
+    kk[r] = qq[r] = 0.f;
+    if (rin) {
+      kk[r] = p.k[(int64_t)w * KA + r0 + r];
+      qq[r] = p.q[(int64_t)w * KA + r0 + r];
+    }
     float x[CPT];
 #pragma unroll
     for (int j = 0; j < CPT; ++j) x[j] = 0.f;
-    if (colok) ld_f32<CPT>(p.h_in + mb + (int64_t)(r0 + r) * p.V + c0, x);
+    if (colok && rin) ld_f32<CPT>(p.h_in + mb + (int64_t)(r0 + r) * p.V + c0, x);
 #pragma unroll
     for (int j = 0; j < CPT; ++j) h[r][j] = x[j] * alpha;
   }
@@ -442,7 +468,8 @@ __global__ __launch_bounds__(kThreadsFor<K>) void fp32_step_kernel(const Fp32Par
   }
   if (colok) {
 #pragma unroll
-    for (int r = 0; r < RPS; ++r) st_f32<CPT>(p.h_out + mb + (int64_t)(r0 + r) * p.V + c0, h[r]);
+    for (int r = 0; r < RPS; ++r)
+      if (!MK || r0 + r < KA) st_f32<CPT>(p.h_out + mb + (int64_t)(r0 + r) * p.V + c0, h[r]);
   }
   __syncthreads();
   if (ks == 0 && colok) {
@@ -453,43 +480,63 @@ __global__ __launch_bounds__(kThreadsFor<K>) void fp32_step_kernel(const Fp32Par
   }
 }
 
-template <int K, int MODE, int CPT>
+template <int K, int MODE, int CPT, bool MK>
 int launch_quant(const StepParams& p, int64_t grid, int res_fmt, hipStream_t s) {
   const dim3 g((unsigned)grid), b(kThreadsFor<K>);
   switch (res_fmt) {
-    case kResFp32: hipLaunchKernelGGL((quant_step_kernel<K, kResFp32, MODE, CPT>), g, b, 0, s, p); break;
-    case kResFp16: hipLaunchKernelGGL((quant_step_kernel<K, kResFp16, MODE, CPT>), g, b, 0, s, p); break;
-    case kResFp8: hipLaunchKernelGGL((quant_step_kernel<K, kResFp8, MODE, CPT>), g, b, 0, s, p); break;
-    default: hipLaunchKernelGGL((quant_step_kernel<K, kResInt8, MODE, CPT>), g, b, 0, s, p); break;
+    case kResFp32: hipLaunchKernelGGL((quant_step_kernel<K, kResFp32, MODE, CPT, MK>), g, b, 0, s, p); break;
+    case kResFp16: hipLaunchKernelGGL((quant_step_kernel<K, kResFp16, MODE, CPT, MK>), g, b, 0, s, p); break;
+    case kResFp8: hipLaunchKernelGGL((quant_step_kernel<K, kResFp8, MODE, CPT, MK>), g, b, 0, s, p); break;
+    default: hipLaunchKernelGGL((quant_step_kernel<K, kResInt8, MODE, CPT, MK>), g, b, 0, s, p); break;
   }
   return check_launch("ck_gdn_quant_step");
 }
 
-template <int MODE, int CPT>
-int launch_quant_k(const StepParams& p, int64_t grid, int K, int res_fmt, hipStream_t s) {
-  switch (K) {
-    case 16: return launch_quant<16, MODE, CPT>(p, grid, res_fmt, s);
-    case 32: return launch_quant<32, MODE, CPT>(p, grid, res_fmt, s);
-    case 64: return launch_quant<64, MODE, CPT>(p, grid, res_fmt, s);
-    case 128: return launch_quant<128, MODE, CPT>(p, grid, res_fmt, s);
-    default: return launch_quant<256, MODE, CPT>(p, grid, res_fmt, s);
+// K padded to KP = max(16, next_pow2(K)) (K <= 256)
+inline int padded_k(int K) {
+  int kp = 16;
+  while (kp < K) kp *= 2;
+  return kp;
+}
+
+template <int MODE, int CPT, bool MK>
+int launch_quant_kp(const StepParams& p, int64_t grid, int KP, int res_fmt, hipStream_t s) {
+  switch (KP) {
+    case 16: return launch_quant<16, MODE, CPT, MK>(p, grid, res_fmt, s);
+    case 32: return launch_quant<32, MODE, CPT, MK>(p, grid, res_fmt, s);
+    case 64: return launch_quant<64, MODE, CPT, MK>(p, grid, res_fmt, s);
+    case 128: return launch_quant<128, MODE, CPT, MK>(p, grid, res_fmt, s);
+    default: return launch_quant<256, MODE, CPT, MK>(p, grid, res_fmt, s);
   }
 }
 
-template <int CPT>
-int launch_fp32(const Fp32Params& p, int64_t grid, int K, hipStream_t s) {
+template <int MODE, int CPT>
+int launch_quant_k(const StepParams& p, int64_t grid, int K, int res_fmt, hipStream_t s) {
+  const int KP = padded_k(K);
+  return KP == K ? launch_quant_kp<MODE, CPT, false>(p, grid, KP, res_fmt, s)
+                 : launch_quant_kp<MODE, CPT, true>(p, grid, KP, res_fmt, s);
+}
+
+template <int CPT, bool MK>
+int launch_fp32_kp(const Fp32Params& p, int64_t grid, int KP, hipStream_t s) {
   const dim3 g((unsigned)grid);
-  switch (K) {
-    case 16: hipLaunchKernelGGL((fp32_step_kernel<16, CPT>), g, dim3(kThreadsFor<16>), 0, s, p); break;
-    case 32: hipLaunchKernelGGL((fp32_step_kernel<32, CPT>), g, dim3(kThreadsFor<32>), 0, s, p); break;
-    case 64: hipLaunchKernelGGL((fp32_step_kernel<64, CPT>), g, dim3(kThreadsFor<64>), 0, s, p); break;
-    case 128: hipLaunchKernelGGL((fp32_step_kernel<128, CPT>), g, dim3(kThreadsFor<128>), 0, s, p); break;
-    default: hipLaunchKernelGGL((fp32_step_kernel<256, CPT>), g, dim3(kThreadsFor<256>), 0, s, p); break;
+  switch (KP) {
+    case 16: hipLaunchKernelGGL((fp32_step_kernel<16, CPT, MK>), g, dim3(kThreadsFor<16>), 0, s, p); break;
+    case 32: hipLaunchKernelGGL((fp32_step_kernel<32, CPT, MK>), g, dim3(kThreadsFor<32>), 0, s, p); break;
+    case 64: hipLaunchKernelGGL((fp32_step_kernel<64, CPT, MK>), g, dim3(kThreadsFor<64>), 0, s, p); break;
+    case 128: hipLaunchKernelGGL((fp32_step_kernel<128, CPT, MK>), g, dim3(kThreadsFor<128>), 0, s, p); break;
+    default: hipLaunchKernelGGL((fp32_step_kernel<256, CPT, MK>), g, dim3(kThreadsFor<256>), 0, s, p); break;
   }
   return check_launch("ck_gdn_fp32_step");
 }
 
-inline bool valid_k(int K) { return K == 16 || K == 32 || K == 64 || K == 128 || K == 256; }
+template <int CPT>
+int launch_fp32(const Fp32Params& p, int64_t grid, int K, hipStream_t s) {
+  const int KP = padded_k(K);
+  return KP == K ? launch_fp32_kp<CPT, false>(p, grid, KP, s) : launch_fp32_kp<CPT, true>(p, grid, KP, s);
+}
+
+inline bool valid_k(int K) { return K >= 1 && K <= 256; }
 
 // Bitwise OR of the addresses: its low bits are zero only if every pointer is
 // aligned that far.
@@ -514,7 +561,7 @@ extern "C" int ck_gdn_quant_step(const int8_t* h_in, const float* scale_in, cons
   using namespace ck;
   using namespace ck::qs;
   if (B < 0 || HV <= 0 || K <= 0 || V <= 0) return fail(CK_EINVAL, "bad sizes B=%d HV=%d K=%d V=%d", B, HV, K, V);
-  if (!valid_k(K)) return fail(CK_EUNSUPPORTED, "K must be one of 16, 32, 64, 128, 256, got %d", K);
+  if (!valid_k(K)) return fail(CK_EUNSUPPORTED, "K must be in 1..256, got %d", K);
   if (res_fmt < CK_RES_FP32 || res_fmt > CK_RES_INT8) return fail(CK_EINVAL, "unknown residual format %d", res_fmt);
   if (quant_mode != CK_QUANT_FAST && quant_mode != CK_QUANT_EXACT)
     return fail(CK_EINVAL, "quant_mode must be CK_QUANT_FAST or CK_QUANT_EXACT, got %d", quant_mode);
@@ -551,6 +598,7 @@ extern "C" int ck_gdn_quant_step(const int8_t* h_in, const float* scale_in, cons
   p.HV = HV;
   p.V = V;
   p.nvt = col_tiles(V, vec ? 4 : 1);
+  p.K = K;
   volatile float one = 1.0f;
   p.qmax = qmax;
   p.rqmax = one / qmax;
@@ -568,13 +616,13 @@ extern "C" int ck_gdn_fp32_step(const float* h_in, const float* q, const float* 
   using namespace ck;
   using namespace ck::qs;
   if (B < 0 || HV <= 0 || K <= 0 || V <= 0) return fail(CK_EINVAL, "bad sizes B=%d HV=%d K=%d V=%d", B, HV, K, V);
-  if (!valid_k(K)) return fail(CK_EUNSUPPORTED, "K must be one of 16, 32, 64, 128, 256, got %d", K);
+  if (!valid_k(K)) return fail(CK_EUNSUPPORTED, "K must be in 1..256, got %d", K);
   if (B == 0) return ok();
   if (!h_in || !q || !k || !v || !alpha || !beta || !o || !h_out) return fail(CK_EINVAL, "null pointer argument");
   const uintptr_t bits = addr_bits(h_in, q, k, v, alpha, beta, o, h_out);
   if (bits & 3) return fail(CK_EINVAL, "fp32 tensors must be 4-byte aligned");
   const bool vec = V % 4 == 0 && (bits & 15) == 0;
-  Fp32Params p{h_in, q, k, v, alpha, beta, o, h_out, V, col_tiles(V, vec ? 4 : 1)};
+  Fp32Params p{h_in, q, k, v, alpha, beta, o, h_out, V, col_tiles(V, vec ? 4 : 1), K};
   const int64_t grid = (int64_t)B * HV * p.nvt;
   if (grid > 0x7fffffff) return fail(CK_EUNSUPPORTED, "grid too large");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);

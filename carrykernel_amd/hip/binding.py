@@ -71,12 +71,10 @@ class HipModule:
         ``e_scale_in`` / ``e_scale_out`` are read / written for the int8
         residual only, and always passed, as in the reference.
 
-        One difference from the CUDA launcher: that kernel loops over any K
-        at run time (.cu:161-166, :185-190), this one takes K in {16, 32,
-        64, 128, 256} (K-slices held in registers, a fixed reduction order
-        per K) and raises ``RuntimeError`` ("K must be ...") for any other
-        K, as the Triton path of statequant/kernel.py:277 (``tl.arange(0,
-        K)``) needs a power of two too."""
+        K is any of 1..256: the CUDA launcher loops over any K at run time
+        (.cu:161-166, :185-190); here rows past K are zero-padded to the next
+        power of two (at least 16), whose K-slices fix the reduction order.
+        K above 256 raises ``RuntimeError`` ("K must be in 1..256")."""
         _check_state(h_in, "h_in")
         _check_state(e_in, "e_in")
         _check(h_in.dtype == torch.int8, "h_in must be int8")
@@ -102,7 +100,7 @@ class HipModule:
 
     def gdn_fp32_step(self, h_in, q, k, v, alpha, beta, o, h_out, block_v: int) -> None:
         """Fused FP32 GDN step into the caller's ``o, h_out`` (.cu:350-371).
-        K in {16, 32, 64, 128, 256}, as for gdn_quant_step."""
+        K in 1..256, as for gdn_quant_step."""
         _check_state(h_in, "h_in")
         _check(h_in.dtype == torch.float32, "h_in must be fp32")
         _check(h_in.dim() == 4, "h_in must be [B, HV, K, V]")

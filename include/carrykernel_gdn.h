@@ -228,7 +228,8 @@ int ck_gdn_packed_decode_float_state(const void* mixed_qkv, int qkv_dtype, int64
  * residual, as the reference's GPU kernels do (cuda/gdn_state_kernel.cu:210,233).
  * e_scale_in / e_scale_out are read / written only for CK_RES_INT8.
  * In-place use (h_out == h_in, e_out == e_in, ...) is allowed.
- * Requirements: K in {16, 32, 64, 128, 256}; any V >= 1; fp32 tensors 4-byte
+ * Requirements: K in 1..256 (rows past K zero-padded to max(16, next_pow2(K)),
+ *   whose K-slices fix the reduction order); any V >= 1; fp32 tensors 4-byte
  * and the residual element-size aligned. V % 4 == 0 with 16-byte aligned
  * tensors takes one vector access per 4 columns, anything else one access
  * per column (statequant/kernel.py:277-279 masks offs_v < V the same way).

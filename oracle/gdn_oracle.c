@@ -464,6 +464,9 @@ void orc_e5m2_to_f32_n(const uint8_t* x, float* y, int64_t n) {
 /* consecutive rows, S = 8 for K <= 128 and K/16 (16 rows each) above; each   */
 /* slice is x0*y0 then fmaf over its rows; the S slice sums combine by a      */
 /* balanced pairwise tree (S = 8: ((s0+s1)+(s2+s3))+((s4+s5)+(s6+s7))).       */
+/* Any K in 1..1024: the rows are zero-padded to KP = max(16, next_pow2(K)),  */
+/* as the reference's Triton kernel masks its BK = next_pow2(K) rows          */
+/* (statequant/kernel.py:277-279), and the sums take KP's slices.             */
 /* ------------------------------------------------------------------------- */
 #define RES_FP32 0
 #define RES_FP16 1
@@ -485,12 +488,13 @@ static float dot_slices(const float* x, int64_t sx, const float* y, int K) {
   return tree_sum(part, ns);
 }
 
-/* K = 16, 32, 64, 128 (8 slices) or a multiple of 16 up to 1024 whose K/16 is a power of two */
-static int statequant_k_ok(int K) {
-  if (K < 16 || K > 1024 || K % 8 != 0) return 0;
-  if (K <= 128) return 1;
-  const int ns = K / 16;
-  return K % 16 == 0 && (ns & (ns - 1)) == 0;
+static int statequant_k_ok(int K) { return K >= 1 && K <= 1024; }
+
+/* KP = max(16, next_pow2(K)): the padded row count whose slices the sums take */
+static int statequant_kp(int K) {
+  int kp = 16;
+  while (kp < K) kp *= 2;
+  return kp;
 }
 
 /* statequant/kernel.py:149-178 (torch reference) and :260-341 (GPU kernel):
@@ -507,7 +511,11 @@ int orc_quant_step_kv(const int8_t* h_in, const float* scale_in, const void* e_i
 #pragma omp parallel
 #endif
   {
-    float* h = (float*)malloc(sizeof(float) * (size_t)K * V);
+    const int KP = statequant_kp(K);
+    /* rows K..KP-1 of h, kp and qp stay +0: zero codes, zero q and k */
+    float* h = (float*)calloc((size_t)KP * V, sizeof(float));
+    float* kp = (float*)calloc((size_t)KP, sizeof(float));
+    float* qp = (float*)calloc((size_t)KP, sizeof(float));
     float* rd = (float*)malloc(sizeof(float) * V);
     float* col = (float*)malloc(sizeof(float) * K);
 #ifdef _OPENMP
@@ -516,17 +524,21 @@ int orc_quant_step_kv(const int8_t* h_in, const float* scale_in, const void* e_i
     for (int64_t w = 0; w < (int64_t)B * HV; ++w) {
       const int64_t mb = w * (int64_t)K * V, vb = w * V, kb = w * K;
       const float a = alpha[w], bt = beta[w];
+      for (int r = 0; r < K; ++r) {
+        kp[r] = k[kb + r];
+        qp[r] = q[kb + r];
+      }
       /* dequantize + decay (kernel.py:165-166) */
       for (int r = 0; r < K; ++r)
         for (int c = 0; c < V; ++c) {
           const float code = (float)h_in[mb + (int64_t)r * V + c];
           h[(int64_t)r * V + c] = mode == MODE_FAST ? code * (scale_in[vb + c] * a) : (code * scale_in[vb + c]) * a;
         }
-      /* delta rule (kernel.py:167-170) */
-      for (int c = 0; c < V; ++c) rd[c] = bt * (v[vb + c] - dot_slices(h + c, V, k + kb, K));
+      /* delta rule (kernel.py:167-170); a padding row stays +0 (its k is 0) */
+      for (int c = 0; c < V; ++c) rd[c] = bt * (v[vb + c] - dot_slices(h + c, V, kp, KP));
       for (int r = 0; r < K; ++r)
         for (int c = 0; c < V; ++c) h[(int64_t)r * V + c] = madd(k[kb + r], rd[c], h[(int64_t)r * V + c], mode);
-      for (int c = 0; c < V; ++c) o[vb + c] = dot_slices(h + c, V, q + kb, K);
+      for (int c = 0; c < V; ++c) o[vb + c] = dot_slices(h + c, V, qp, KP);
       /* residual add (kernel.py:172) */
       for (int r = 0; r < K; ++r)
         for (int c = 0; c < V; ++c) {
@@ -575,6 +587,8 @@ int orc_quant_step_kv(const int8_t* h_in, const float* scale_in, const void* e_i
       }
     }
     free(h);
+    free(kp);
+    free(qp);
     free(rd);
     free(col);
   }
@@ -585,17 +599,28 @@ int orc_quant_step_kv(const int8_t* h_in, const float* scale_in, const void* e_i
 int orc_fp32_step_kv(const float* h_in, const float* q, const float* k, const float* v, const float* alpha,
                      const float* beta, float* o, float* h_out, int B, int HV, int K, int V) {
   if (!statequant_k_ok(K) || V <= 0) return 1;
+  const int KP = statequant_kp(K);
   float* rd = (float*)malloc(sizeof(float) * V);
+  float* h = (float*)calloc((size_t)KP * V, sizeof(float)); /* rows K..KP-1 stay +0 */
+  float* kp = (float*)calloc((size_t)KP, sizeof(float));
+  float* qp = (float*)calloc((size_t)KP, sizeof(float));
   for (int64_t w = 0; w < (int64_t)B * HV; ++w) {
     const int64_t mb = w * (int64_t)K * V, vb = w * V, kb = w * K;
-    float* h = h_out + mb;
+    for (int r = 0; r < K; ++r) {
+      kp[r] = k[kb + r];
+      qp[r] = q[kb + r];
+    }
     for (int64_t i = 0; i < (int64_t)K * V; ++i) h[i] = h_in[mb + i] * alpha[w];
-    for (int c = 0; c < V; ++c) rd[c] = beta[w] * (v[vb + c] - dot_slices(h + c, V, k + kb, K));
+    for (int c = 0; c < V; ++c) rd[c] = beta[w] * (v[vb + c] - dot_slices(h + c, V, kp, KP));
     for (int r = 0; r < K; ++r)
       for (int c = 0; c < V; ++c) h[(int64_t)r * V + c] = fmaf(k[kb + r], rd[c], h[(int64_t)r * V + c]);
-    for (int c = 0; c < V; ++c) o[vb + c] = dot_slices(h + c, V, q + kb, K);
+    for (int c = 0; c < V; ++c) o[vb + c] = dot_slices(h + c, V, qp, KP);
+    for (int64_t i = 0; i < (int64_t)K * V; ++i) h_out[mb + i] = h[i];
   }
   free(rd);
+  free(h);
+  free(kp);
+  free(qp);
   return 0;
 }
 

@@ -169,9 +169,16 @@ def packed_decode(mixed, a, b, A_log, dt_bias, scale, sc, ss, rc, rs, idx, H, *,
 
 
 def quant_step_kv(h_int8, scale, e, e_scale, q, k, v, alpha, beta, *, bits, res_fmt, exact):
-    """One statequant-layout step; residual storage as in oracle.quant_step_kv."""
+    """One statequant-layout step; residual storage as in oracle.quant_step_kv.
+    Any K: the sums run over KP = max(16, next_pow2(K)) rows, zero past K, as
+    the reference's Triton kernel masks its BK = next_pow2(K) rows
+    (statequant/kernel.py:277-279)."""
     B, HV, K, V = h_int8.shape
-    rows = K // 8 if K <= 128 else 16          # rows per K-slice
+    KP = 16
+    while KP < K:
+        KP *= 2
+    rows = KP // 8 if KP <= 128 else 16        # rows per K-slice
+    Z = [F(0.0)] * (KP - K)
     qmax = F(2 ** (bits - 1) - 1)
     o = np.zeros((B, HV, V), F)
     h_out = np.zeros_like(h_int8)
@@ -181,17 +188,17 @@ def quant_step_kv(h_int8, scale, e, e_scale, q, k, v, alpha, beta, *, bits, res_
     for bb in range(B):
         for hv in range(HV):
             al, be = F(alpha[bb, hv]), F(beta[bb, hv])
-            kk = [F(x) for x in k[bb, hv]]
-            qq = [F(x) for x in q[bb, hv]]
+            kk = [F(x) for x in k[bb, hv]] + Z
+            qq = [F(x) for x in q[bb, hv]] + Z
             for c in range(V):
                 sc = F(scale[bb, hv, c])
                 if exact:
                     h = [F(F(F(int(h_int8[bb, hv, r, c])) * sc) * al) for r in range(K)]
                 else:
                     h = [F(F(int(h_int8[bb, hv, r, c])) * F(sc * al)) for r in range(K)]
-                dv = F(be * F(F(v[bb, hv, c]) - chunk_dot(h, kk, rows)))
+                dv = F(be * F(F(v[bb, hv, c]) - chunk_dot(h + Z, kk, rows)))
                 h = [madd(kk[r], dv, h[r], exact) for r in range(K)]
-                o[bb, hv, c] = chunk_dot(h, qq, rows)
+                o[bb, hv, c] = chunk_dot(h + Z, qq, rows)
                 if res_fmt == oracle.RES_INT8:
                     t = [madd(F(int(e[bb, hv, r, c])), F(e_scale[bb, hv, c]), h[r], exact) for r in range(K)]
                 elif res_fmt == oracle.RES_FP16:

@@ -98,14 +98,16 @@ def test_packed_decode_empty_batch_with_null_pointers(L):
 
 def test_other_entry_points_argument_errors(L):
     p = ctypes.c_void_p(16)
-    rc = L.ck_gdn_quant_step(p, p, p, p, p, p, p, p, p, p, p, p, p, p, 1, 1, 24, 8, 127.0, 0, 0, None)
-    assert rc == _native.CK_EUNSUPPORTED and "K must be" in L.ck_last_error().decode()
-    rc = L.ck_gdn_quant_step(p, p, p, p, p, p, p, p, p, p, p, p, p, p, 1, 1, 512, 6, 127.0, 0, 0, None)
-    assert rc == _native.CK_EUNSUPPORTED and "K must be" in L.ck_last_error().decode()
-    # unlike the CUDA launcher (any K), the statequant step takes K in {16 .. 256}, powers of two
-    for k_bad in (48, 96, 100):
+    # the statequant step takes any K in 1..256 (rows zero-padded to a power of two); B = 0 checks and
+    # launches nothing, so these run without a GPU
+    for k_ok in (1, 24, 48, 96, 100, 256):
+        assert L.ck_gdn_quant_step(p, p, p, p, p, p, p, p, p, p, p, p, p, p, 0, 1, k_ok, 6, 127.0, 0, 0, None) == 0
+        assert L.ck_gdn_fp32_step(p, p, p, p, p, p, p, p, 0, 1, k_ok, 6, None) == 0
+    for k_bad in (257, 512):
         rc = L.ck_gdn_quant_step(p, p, p, p, p, p, p, p, p, p, p, p, p, p, 1, 1, k_bad, 6, 127.0, 0, 0, None)
-        assert rc == _native.CK_EUNSUPPORTED and "K must be" in L.ck_last_error().decode()
+        assert rc == _native.CK_EUNSUPPORTED and "K must be in 1..256" in L.ck_last_error().decode()
+        rc = L.ck_gdn_fp32_step(p, p, p, p, p, p, p, p, 1, 1, k_bad, 6, None)
+        assert rc == _native.CK_EUNSUPPORTED and "K must be in 1..256" in L.ck_last_error().decode()
     odd = ctypes.c_void_p(17)   # an fp16 residual at an odd address
     rc = L.ck_gdn_quant_step(p, p, odd, p, p, p, p, p, p, p, p, p, p, p, 1, 1, 32, 6, 127.0, 1, 0, None)
     assert rc == _native.CK_EINVAL and "2-byte aligned" in L.ck_last_error().decode()
@@ -113,7 +115,7 @@ def test_other_entry_points_argument_errors(L):
     assert rc == _native.CK_EINVAL and "qmax" in L.ck_last_error().decode()
     rc = L.ck_gdn_quant_step(p, p, p, None, p, p, p, p, p, p, p, p, p, None, 1, 1, 32, 8, 127.0, 3, 0, None)
     assert rc == _native.CK_EINVAL and "e_scale" in L.ck_last_error().decode()
-    rc = L.ck_gdn_fp32_step(p, p, p, p, p, p, p, p, 1, 1, 48, 8, None)
+    rc = L.ck_gdn_fp32_step(p, p, p, p, p, p, p, p, 1, 1, 300, 8, None)
     assert rc == _native.CK_EUNSUPPORTED
     rc = L.ck_quantize_rows(p, 9, 128, 4, 128, 127.0, p, p, None)
     assert rc == _native.CK_EINVAL

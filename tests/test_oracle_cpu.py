@@ -218,10 +218,11 @@ def test_any_k_step_equals_zero_padded_power_of_two(K, KP, resid_fmt, per_head, 
 
 @pytest.mark.parametrize("res_fmt", [oracle.RES_FP32, oracle.RES_FP16, oracle.RES_FP8, oracle.RES_INT8])
 @pytest.mark.parametrize("exact", [False, True])
-@pytest.mark.parametrize("HV,K,V", [(2, 16, 4), (1, 64, 5), (1, 256, 3)])
+@pytest.mark.parametrize("HV,K,V", [(2, 16, 4), (1, 64, 5), (1, 256, 3), (2, 7, 4), (1, 100, 3), (1, 200, 2)])
 def test_quant_step_kv_matches_bruteforce(res_fmt, exact, HV, K, V):
     """Every residual format and mode; K = 256 takes 16 slices of 16 rows,
-    smaller K 8 slices of K/8; V not a multiple of 4."""
+    smaller K 8 slices of K/8; V not a multiple of 4. K = 7, 100, 200: the
+    sums over the rows zero-padded to 16, 128 and 256."""
     B = 1
     rng = np.random.default_rng(res_fmt + K)
     h0 = (rng.standard_normal((B, HV, K, V)) * 0.1).astype(F)
@@ -250,6 +251,58 @@ def test_quant_step_kv_matches_bruteforce(res_fmt, exact, HV, K, V):
             assert g is None
         else:
             np.testing.assert_array_equal(g, r)
+
+
+@pytest.mark.parametrize("res_fmt", [oracle.RES_FP32, oracle.RES_FP16, oracle.RES_FP8, oracle.RES_INT8])
+@pytest.mark.parametrize("K,KP", [(5, 16), (48, 64), (100, 128), (130, 256)])
+def test_statequant_any_k_equals_zero_padded_power_of_two(res_fmt, K, KP):
+    """An any-K statequant step equals the KP step on the same rows followed
+    by zero rows (zero codes, residual, q and k): o, scales and the first K
+    rows of codes and residual agree bit for bit, and the padding rows come
+    out zero."""
+    B, HV, V = 2, 2, 6
+    rng = np.random.default_rng(K + res_fmt)
+    h0 = (rng.standard_normal((B, HV, K, V)) * 0.1).astype(F)
+    codes, scale = oracle.quantize_cols(h0)
+    res = (rng.standard_normal((B, HV, K, V)) * 1e-3).astype(F)
+    es = None
+    if res_fmt == oracle.RES_INT8:
+        es = (np.abs(res).max(axis=-2) / 127).astype(F)
+        e = np.clip(np.rint(res / es[:, :, None, :]), -127, 127).astype(np.int8)
+    elif res_fmt == oracle.RES_FP16:
+        e = res.astype(np.float16).view(np.uint16)
+    elif res_fmt == oracle.RES_FP8:
+        e = oracle.f32_to_e5m2_bits(res)
+    else:
+        e = res
+    q = rng.standard_normal((B, HV, K)).astype(F)
+    k = rng.standard_normal((B, HV, K)).astype(F)
+    v = rng.standard_normal((B, HV, V)).astype(F)
+    alpha = F(rng.uniform(0.9, 1.0, (B, HV)))
+    beta = F(rng.uniform(0.1, 0.9, (B, HV)))
+
+    def pad_rows(x):
+        z = np.zeros(x.shape[:2] + (KP - K,) + x.shape[3:], x.dtype)
+        return np.ascontiguousarray(np.concatenate([x, z], axis=2))
+
+    for mode in (oracle.MODE_FAST, oracle.MODE_EXACT):
+        got = oracle.quant_step_kv(codes, scale, e, es, q, k, v, alpha, beta, bits=8, res_fmt=res_fmt, mode=mode)
+        ref = oracle.quant_step_kv(pad_rows(codes), scale, pad_rows(e), es, pad_rows(q), pad_rows(k), v, alpha, beta,
+                                   bits=8, res_fmt=res_fmt, mode=mode)
+        o, h_out, s_out, e_out, es_out = got
+        o_p, h_p, s_p, e_p, es_p = ref
+        np.testing.assert_array_equal(o, o_p)
+        np.testing.assert_array_equal(s_out, s_p)
+        np.testing.assert_array_equal(h_out, h_p[:, :, :K])
+        np.testing.assert_array_equal(e_out, e_p[:, :, :K])
+        assert not h_p[:, :, K:].any() and not np.asarray(e_p[:, :, K:]).view(np.uint8).any()
+        if es_out is not None:
+            np.testing.assert_array_equal(es_out, es_p)
+    h, o = oracle.fp32_step_kv(h0, q, k, v, alpha, beta)
+    h_p, o_p = oracle.fp32_step_kv(pad_rows(h0), pad_rows(q), pad_rows(k), v, alpha, beta)
+    np.testing.assert_array_equal(o, o_p)
+    np.testing.assert_array_equal(h, h_p[:, :, :K])
+    assert not h_p[:, :, K:].any()
 
 
 def _slice_order_case(K, V, rows):

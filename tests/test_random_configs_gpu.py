@@ -127,12 +127,15 @@ def _run_decode(device, seed, c):
 @pytest.mark.parametrize("seed", range(24))
 def test_random_statequant_step_bit_exact(device, seed):
     """The statequant-layout step (ck_gdn_quant_step through gdn_quant_step_fused)
-    on random shapes, residual formats, quant modes and state bits."""
+    on random shapes, residual formats, quant modes and state bits; from seed
+    16 on, K anywhere in 1..256 (rows zero-padded to a power of two)."""
     from carrykernel_amd.statequant import kernel as sq
     from tests.test_statequant_gpu import _random_state, _storage, make_inputs
 
     rng = np.random.default_rng(5000 + seed)
     K = int(rng.choice([16, 32, 64, 128, 256]))
+    if seed >= 16:
+        K = int(rng.integers(1, 257))
     # half the draws a multiple of 4 (vector column groups), half any V
     V = 4 * int(rng.integers(1, 50)) if rng.random() < 0.5 else int(rng.integers(1, 200))
     B, HV = int(rng.integers(1, 4)), int(rng.integers(1, 9))

@@ -60,11 +60,13 @@ def _random_state(B, HV, K, V, res_fmt, seed, bits=8):
 @pytest.mark.parametrize("mode", ["fast", "exact"])
 @pytest.mark.parametrize("K,V,B,HV", [(128, 128, 2, 32), (64, 64, 1, 4), (32, 8, 1, 1), (16, 136, 2, 3),
                                      (256, 128, 1, 4), (128, 130, 1, 3), (256, 130, 2, 2), (16, 3, 2, 2),
-                                     (64, 67, 1, 2), (16, 1, 3, 1)])
+                                     (64, 67, 1, 2), (16, 1, 3, 1), (48, 128, 2, 4), (100, 67, 1, 3),
+                                     (7, 8, 2, 2), (200, 128, 1, 2), (1, 5, 2, 2)])
 def test_step_bit_exact_vs_oracle(device, res_fmt, mode, K, V, B, HV):
     """K = 256 runs 16 slices of 16 rows; V not a multiple of 4 (130, 3, 67,
     and a single column) takes the per-column access path with a partial last
-    column group."""
+    column group. K = 48, 100, 7, 200, 1: rows zero-padded to 64, 128, 16,
+    256, 16 (the oracle pads the same way)."""
     h_int8, scale, e, es = _random_state(B, HV, K, V, res_fmt, seed=K + V + res_fmt)
     _, q, k, v, alpha, beta = make_inputs(1, B, HV, K, V, seed=5)
     beta = beta[0] * 0 + torch.rand(B, HV, generator=torch.Generator().manual_seed(9))
@@ -100,7 +102,8 @@ def test_int6_state_int8_residual(device):
     assert int(got[1].abs().max()) <= 31 and int(got[3].abs().max()) <= 31
 
 
-@pytest.mark.parametrize("K,V", [(128, 128), (32, 8), (256, 128), (256, 130), (64, 3)])
+@pytest.mark.parametrize("K,V", [(128, 128), (32, 8), (256, 128), (256, 130), (64, 3), (48, 128), (100, 67),
+                                 (200, 130), (3, 4)])
 def test_fp32_step_bit_exact(device, K, V):
     h0, q, k, v, alpha, beta = make_inputs(1, 2, 4, K, V, seed=7)
     h_g, o_g = binding.gdn_fp32_step_hip(h0.to(device), q[0].to(device), k[0].to(device), v[0].to(device),
