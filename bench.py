@@ -926,6 +926,33 @@ def drift_c5(device, bits, tokens=2048, layers=24, B=64, every=256, resid_fmt=No
     return rows
 
 
+def _single_item_timeline(B, resid_fmt, per_head, rel, start, begin, data, end, cu_id):
+    """Timeline summary of a launch of the one-item kernel (one workgroup per
+    item, started by the dispatcher as CU slots free): when workgroups start,
+    each one's chain from its start to its end, and when each CU finishes."""
+    import numpy as np
+    st = rel[:, 0]
+    cus = np.unique(cu_id)
+    first_wave = np.array([int(np.count_nonzero((cu_id == c) & (st < np.nanmin(st) + 0.5))) for c in cus])
+    cu_end = np.array([np.nanmax(end[cu_id == c]) for c in cus])
+    pct = lambda x, q: round(float(np.nanpercentile(x, q)), 2)   # noqa: E731
+    return {"workload": f"B={B} {'int4' if resid_fmt == qpd.RESID_INT4 else 'int8'} residual, "
+                        f"{'per-head' if per_head else 'per-row'} scale",
+            "kernel": "packed_decode_single_kernel (one item per workgroup)",
+            "workgroups": int(len(st)), "cus": int(len(cus)),
+            "started_within_0.5us_per_cu_median": float(np.median(first_wave)),
+            "start_us": {"p50": pct(st, 50), "p90": pct(st, 90), "max": pct(st, 100)},
+            "from_start_us": {"slot_id_known": pct(start[:, 0] - st, 50),
+                              "loads_issued": pct(start[:, 1] - st, 50),
+                              "gates_done": pct(start[:, 2] - st, 50),
+                              "data_in": pct(data - st, 50), "end": pct(end - st, 50),
+                              "end_p10": pct(end - st, 10), "end_p90": pct(end - st, 90)},
+            "compute_us": {"p50": pct(end - data, 50), "p90": pct(end - data, 90)},
+            "cu_last_end_us": {"p50": round(float(np.median(cu_end)), 2), "p90": round(float(np.percentile(cu_end, 90)), 2),
+                               "max": round(float(cu_end.max()), 2)},
+            "span_us": round(float(np.nanmax(end)), 2)}
+
+
 def timeline_report(device, B, resid_fmt, per_head, groups, launches=20):
     """Per-workgroup timeline of one launch of the headline step, from the
     timestamped measurement build (libcarrykernel_gdn_timeline.so): the last
@@ -955,7 +982,7 @@ def timeline_report(device, B, resid_fmt, per_head, groups, launches=20):
     for t in range(200):
         step(t)
     torch.cuda.synchronize()
-    slots, max_wg = 40, 2048
+    slots, max_wg = 40, 8192
     buf = torch.zeros(max_wg * slots, dtype=torch.int64, device=device)
     _native.check(L.ck_timeline_set(buf.data_ptr()), "ck_timeline_set")
     for t in range(launches - 1):
@@ -977,6 +1004,9 @@ def timeline_report(device, B, resid_fmt, per_head, groups, launches=20):
     per_cu = int(np.bincount(np.unique(cu_id, return_inverse=True)[1]).max())
     begin, data, end = rel[:, 1:31:3], rel[:, 2:31:3], rel[:, 3:31:3]
     n_rec = np.sum(~np.isnan(end), axis=1)
+    if int(n_rec.max()) == 1:
+        return {"timeline": _single_item_timeline(B, resid_fmt, per_head, rel, start, begin[:, 0], data[:, 0],
+                                                  end[:, 0], cu_id)}
     last_end = np.array([end[i, n_rec[i] - 1] for i in range(nwg)])
     comp = np.nansum(end - data, axis=1) / n_rec
     wait = np.nansum(data - begin, axis=1) / n_rec

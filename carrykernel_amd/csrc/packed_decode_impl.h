@@ -654,7 +654,7 @@ __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCo
 // first item's slot id is known, 33 once its loads are issued, 34 once the
 // first gates are computed.
 constexpr int kTlSlots = 40;
-constexpr int kTlMaxWorkgroups = 2048;
+constexpr int kTlMaxWorkgroups = 8192;
 
 __device__ __forceinline__ void tl_mark(const PackedParams& p, int slot) {
 #if CK_TIMELINE
@@ -864,6 +864,17 @@ inline PackedParams requests_from(const PackedParams& p, int n0) {
 template <int RPL, int WAVES>
 constexpr int kMinWavesPerEU = (RPL == 2 && (WAVES == 8 || WAVES == 4)) ? 4 : 1;
 
+// The one-item kernel's register budget: the per-head 8-wave shape at 80
+// VGPRs (six waves per SIMD: three workgroups per CU), others as above.
+template <int RPL, int WAVES, bool PER_HEAD>
+constexpr int kSingleWavesPerEU = (PER_HEAD && RPL == 2 && WAVES == 8) ? 6 : kMinWavesPerEU<RPL, WAVES>;
+
+// Shapes for which a launch of more items than resident workgroups also takes
+// the one-item kernel when it fits more workgroups per CU (see
+// packed_decode_single_kernel): per head at K=128, per row from K=64.
+template <int K, bool PER_HEAD>
+constexpr bool kSingleForLarge = PER_HEAD ? K == 128 : K >= 64;
+
 template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ACT, bool DST>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(kMinWavesPerEU<RPL, WAVES>)))
 void packed_decode_kernel(const int32_t* __restrict__ idx, int items, int stride_idx, uint32_t nvt_d, uint32_t nvt_m,
@@ -941,15 +952,30 @@ void packed_decode_kernel(const int32_t* __restrict__ idx, int items, int stride
   }
 }
 
-// A launch with no more items than resident workgroups: one item per
-// workgroup, its loads, the gates, the item, with no prefetch of a next item.
-// The persistent kernel's loop would issue a past-the-end prefetch before the
-// item and, at the joins of its conditional stores, wait for some of those
-// loads; this kernel has no younger loads to wait for (graph-replayed, int4,
-// HV=32, us: per head B=1 5.70 -> 5.13, B=8 6.89 -> 6.36; per row B=1 4.53 ->
-// 4.01; the same code computes the item, so the results are the same bits).
+// One item per workgroup: its loads, the gates, the item, with no prefetch of
+// a next item; the grid is one workgroup per item and the hardware dispatcher
+// starts the next one on whichever CU frees a slot. Used (launch_cfg) when a
+// launch has no more items than resident workgroups, and for the shapes where
+// this kernel holds more workgroups per CU than the persistent one does with
+// its second register set (kSingleForLarge).
+//  * Small launches: the persistent loop would issue a past-the-end prefetch
+//    before the item and, at the joins of its conditional stores, wait for
+//    some of those loads; this kernel has no younger loads to wait for
+//    (graph-replayed, int4, HV=32, us: per head B=1 5.70 -> 5.13, B=8 6.89 ->
+//    6.36; per row B=1 4.53 -> 4.01).
+//  * Larger launches: at K=128 per head it takes 80 VGPRs, three 8-wave
+//    workgroups per CU against the persistent kernel's two (128 VGPRs), and
+//    per row 56-62 VGPRs, eight 4-wave workgroups against four; the
+//    dispatcher then also balances the end of the launch across CUs (two A/B
+//    pairs on one box, us: per head B=64 28.57 -> 28.15, B=128 48.80 -> 47.24,
+//    B=256 86.49 -> 85.08; per row B=64 28.07 -> 26.81, B=128 47.74 -> 46.49;
+//    per row K=64 B=64 16.03 -> 15.27). Per head at K=32 and 64 it measured
+//    2-3 % slower, and with the int8 residual the head's 64 KB LDS table
+//    keeps it at two workgroups per CU, so those stay persistent.
+// process_item computes the item in both kernels, so the results are the same
+// bits.
 template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ACT, bool DST>
-__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(kMinWavesPerEU<RPL, WAVES>)))
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(kSingleWavesPerEU<RPL, WAVES, PER_HEAD>)))
 void packed_decode_single_kernel(const int32_t* __restrict__ idx, int items, int stride_idx, uint32_t nvt_d,
                                  uint32_t nvt_m, uint32_t nvt_sh, uint32_t hv_d, uint32_t hv_m, uint32_t hv_sh,
                                  int share_n, uint32_t shares, int grid, const PackedParams p,
@@ -1019,7 +1045,14 @@ int launch_cfg(PackedParams p, int B, hipStream_t stream) {
   }
   // fewest items per workgroup, then the fewest workgroups achieving it
   const int per_wg = (p.items + resident - 1) / resident;
-  if (per_wg == 1) {
+  bool single = per_wg == 1;
+  if (!single && kSingleForLarge<K, PER_HEAD>) {
+    int single_per_cu = 0;
+    const void* sfn = reinterpret_cast<const void*>(packed_decode_single_kernel<K, RPL, WAVES, RESID, PER_HEAD, MODE,
+                                                                               ACT, DST>);
+    single = resident_workgroups(sfn, WAVES * 64, &single_per_cu) > 0 && single_per_cu > per_cu;
+  }
+  if (single) {
     hipLaunchKernelGGL((packed_decode_single_kernel<K, RPL, WAVES, RESID, PER_HEAD, MODE, ACT, DST>),
                        dim3((unsigned)p.items), dim3(WAVES * 64), 0, stream, p.idx, p.items, p.stride_idx,
                        p.div_nvt.d, p.div_nvt.m, p.div_nvt.sh, p.div_hv.d, p.div_hv.m, p.div_hv.sh, 0, 0u, p.items,

@@ -78,14 +78,17 @@ def test_c3_b256_bit_exact(device):
                     False, f"C3 B=256 step {t}")
 
 
-@pytest.mark.parametrize("resid_fmt,per_head,mode", [(oracle.RESID_INT4, True, oracle.MODE_FAST),
+@pytest.mark.parametrize("resid_fmt,per_head,mode", [(oracle.RESID_INT8, True, oracle.MODE_FAST),
+                                                     (oracle.RESID_INT4, True, oracle.MODE_FAST),
                                                      (oracle.RESID_INT8, False, oracle.MODE_EXACT)])
 def test_more_than_64_items_per_workgroup(device, resid_fmt, per_head, mode):
-    """B=1100 requests x 32 heads: the persistent grid (at most four
-    workgroups per CU on 256 CUs) gives every workgroup more than 64 items,
-    so a second wave stages the gates of items 64..; the per-row shape's
-    70,400 items exceed what one launch holds (256 per workgroup), so the
-    requests are split over two launches. GQA (H=16), the in-kernel L2 norm,
+    """B=1100 requests x 32 heads. The int8 per-head step runs the
+    persistent kernel (two workgroups per CU on 256 CUs), which gives every
+    workgroup more than 64 items, so a second wave stages the gates of items
+    64..; the int4 per-head step runs the one-item kernel over 35,200
+    workgroups; the per-row shape's 70,400 items exceed what one launch holds
+    (256 per resident persistent workgroup), so the requests are split over
+    two launches of the one-item kernel. GQA (H=16), the in-kernel L2 norm,
     every item checked bit for bit."""
     B = 1100
     S = B + 1
