@@ -1031,7 +1031,20 @@ int launch_cfg(PackedParams p, int B, hipStream_t stream) {
   int per_cu = 0;
   const int resident = resident_workgroups(reinterpret_cast<const void*>(fn), WAVES * 64, &per_cu);
   if (resident <= 0) return fail(CK_ELAUNCH, "cannot query the device occupancy");
-  const int64_t cap = launch_item_cap(resident, per_cu);
+  // the one-item kernel (packed_decode_single_kernel): for a launch with no
+  // more items than resident workgroups, and for larger launches of the
+  // kSingleForLarge shapes when it fits more workgroups per CU
+  bool single = items <= resident;
+  if (!single && kSingleForLarge<K, PER_HEAD>) {
+    int single_per_cu = 0;
+    const void* sfn = reinterpret_cast<const void*>(packed_decode_single_kernel<K, RPL, WAVES, RESID, PER_HEAD, MODE,
+                                                                               ACT, DST>);
+    single = resident_workgroups(sfn, WAVES * 64, &single_per_cu) > 0 && single_per_cu > per_cu;
+  }
+  // the persistent kernel's gate table bounds its items per launch; the
+  // one-item kernel has no table, so only a process-wide limit splits it
+  const int64_t override_cap = max_items_override();
+  const int64_t cap = single ? (override_cap > 0 ? override_cap : items) : launch_item_cap(resident, per_cu);
   if (items > cap) {  // consecutive launches over slices of the requests
     const int64_t per_request = (int64_t)p.HV * nvt;
     if (per_request > cap) return fail(CK_EUNSUPPORTED, "%lld work items per request is too many", (long long)per_request);
@@ -1043,15 +1056,6 @@ int launch_cfg(PackedParams p, int B, hipStream_t stream) {
     }
     return ok();
   }
-  // fewest items per workgroup, then the fewest workgroups achieving it
-  const int per_wg = (p.items + resident - 1) / resident;
-  bool single = per_wg == 1;
-  if (!single && kSingleForLarge<K, PER_HEAD>) {
-    int single_per_cu = 0;
-    const void* sfn = reinterpret_cast<const void*>(packed_decode_single_kernel<K, RPL, WAVES, RESID, PER_HEAD, MODE,
-                                                                               ACT, DST>);
-    single = resident_workgroups(sfn, WAVES * 64, &single_per_cu) > 0 && single_per_cu > per_cu;
-  }
   if (single) {
     hipLaunchKernelGGL((packed_decode_single_kernel<K, RPL, WAVES, RESID, PER_HEAD, MODE, ACT, DST>),
                        dim3((unsigned)p.items), dim3(WAVES * 64), 0, stream, p.idx, p.items, p.stride_idx,
@@ -1059,6 +1063,8 @@ int launch_cfg(PackedParams p, int B, hipStream_t stream) {
                        p, p.dst_idx);
     return check_launch("ck_gdn_packed_decode");
   }
+  // fewest items per workgroup, then the fewest workgroups achieving it
+  const int per_wg = (p.items + resident - 1) / resident;
   const int grid = (p.items + per_wg - 1) / per_wg;
   set_cu_shares(p, grid, resident, per_cu);
   hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(WAVES * 64), 0, stream, p.idx, p.items, p.stride_idx, p.div_nvt.d,

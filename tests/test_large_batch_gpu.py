@@ -5,10 +5,11 @@ more than one wave) or that the step is split over consecutive launches
 
 * C3 at B=256 (HV=32, K=V=128, int4 residual with a per-head scale), two
   steps bit for bit against the oracle;
-* B=1100 through the quantized decode (per-head int4 FAST: one launch,
-  more than 64 items per workgroup; per-row int8 EXACT: 70,400 items, two
-  launches) and through the bf16-state arm (two launches): every item is
-  checked bit for bit;
+* B=1100 through the quantized decode (per-head int8 FAST on the
+  persistent kernel: one launch, more than 64 items per workgroup; per-head
+  int4 FAST and per-row int8 EXACT on the one-item kernel: one launch of
+  35,200 / 70,400 workgroups) and through the bf16-state arm (two
+  launches): every item is checked bit for bit;
 * small steps split into launches of a few items (a limit lowered through
   ck_set_max_items_per_launch) with bf16 activations and output,
   strided ids and out-of-place destinations;
@@ -85,10 +86,9 @@ def test_more_than_64_items_per_workgroup(device, resid_fmt, per_head, mode):
     """B=1100 requests x 32 heads. The int8 per-head step runs the
     persistent kernel (two workgroups per CU on 256 CUs), which gives every
     workgroup more than 64 items, so a second wave stages the gates of items
-    64..; the int4 per-head step runs the one-item kernel over 35,200
-    workgroups; the per-row shape's 70,400 items exceed what one launch holds
-    (256 per resident persistent workgroup), so the requests are split over
-    two launches of the one-item kernel. GQA (H=16), the in-kernel L2 norm,
+    64..; the int4 per-head and the per-row int8 steps run the one-item
+    kernel over 35,200 and 70,400 workgroups in one launch (it has no gate
+    table, so no per-launch item limit). GQA (H=16), the in-kernel L2 norm,
     every item checked bit for bit."""
     B = 1100
     S = B + 1
