@@ -93,6 +93,16 @@ def test_bit_exact_full_occupancy(device, resid_fmt, per_head, B):
               mode="fast", l2norm=False, T=2)
 
 
+@pytest.mark.parametrize("per_head,mode,act", [(True, "exact", torch.bfloat16), (True, "fast", torch.float16),
+                                               (False, "exact", torch.bfloat16)])
+def test_one_item_kernel_at_full_occupancy(device, per_head, mode, act):
+    """More items than resident workgroups on the one-item kernel (int4 at
+    K=128, per head and per row): 16-bit activations and outputs, the
+    in-kernel L2 norm and both modes, B=64 at HV=32, GQA (H=8)."""
+    _run_both(device, B=64, H=8, HV=32, K=128, V=128, resid_fmt=qpd.RESID_INT4, per_head=per_head, mode=mode,
+              l2norm=True, T=2, seed=7 + per_head, act_dtype=act, out_dtype=act)
+
+
 @pytest.mark.parametrize("K,resid_fmt,mode,act", [
     (128, qpd.RESID_INT8, "exact", torch.float32),   # int8 per head: its 64 KB LDS table allows two
     (128, qpd.RESID_INT8, "fast", torch.bfloat16),   # workgroups per CU in either kernel
