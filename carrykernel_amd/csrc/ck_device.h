@@ -61,6 +61,19 @@ __device__ __forceinline__ ActBits load_act_bits(const void* p, int64_t i, int d
   return r;
 }
 
+// load_act_bits without a branch on the dtype: the element's byte offset is
+// selected, so a uniform index gives one scalar load whatever the dtype (a
+// load in each arm of a dtype branch would be joined by a copy that waits for
+// it). An fp32 element is 4-byte aligned (as every float is), so hi is 0 for it.
+__device__ __forceinline__ ActBits load_act_bits_sel(const void* p, int64_t i, int dtype) {
+  const char* e = static_cast<const char*>(p) + (dtype == kF32 ? 4 * i : 2 * i);
+  const uint32_t mis = (uint32_t)reinterpret_cast<uintptr_t>(e) & 3u;  // 0 or 2
+  ActBits r;
+  r.word = *reinterpret_cast<const uint32_t*>(e - mis);
+  r.hi = mis >> 1;
+  return r;
+}
+
 __device__ __forceinline__ float decode_act_bits(ActBits b, int dtype) {
   if (dtype == kF32) return __uint_as_float(b.word);
   const uint32_t h16 = b.hi ? (b.word >> 16) : (b.word & 0xffffu);

@@ -819,6 +819,36 @@ __device__ __forceinline__ void gates_for_items(const PackedParams& p, const Geo
 constexpr int kGateCap = 256;
 constexpr int kWaitVmcnt0 = 0x0f70;  // s_waitcnt simm16: vmcnt 0, expcnt 7, lgkmcnt 15 (vector memory only)
 
+// One item's gates into s_gate[0], for the kernels with one item per
+// workgroup: every wave issues the item's four gate-input loads (uniform
+// addresses: scalar loads, which retire independently of the vector loads)
+// before the item's own loads; wave 0 evaluates the gates once those arrive,
+// while the item's bytes are still in flight (graph-replayed, int4 per head,
+// HV=32, us: B=1 5.35 -> 5.09, B=8 6.33 -> 5.82, B=64 25.06 -> 24.58, three
+// A/B pairs), against loading them after the item and evaluating them lane-
+// parallel as stage_gates does. The caller issues its item's loads between
+// the two calls and passes a barrier before reading s_gate[0].
+struct GateBits {
+  ActBits a, b, A_log, dt_bias;
+};
+
+__device__ __forceinline__ GateBits load_item_gate_bits(const PackedParams& p, const ItemCoord& ic) {
+  return GateBits{load_act_bits_sel(p.a, (int64_t)ic.n * p.stride_a + ic.hv, p.a_dtype()),
+                  load_act_bits_sel(p.b, (int64_t)ic.n * p.stride_b + ic.hv, p.b_dtype()),
+                  load_act_bits_sel(p.A_log, ic.hv, p.A_log_dtype()),
+                  load_act_bits_sel(p.dt_bias, ic.hv, p.dt_bias_dtype())};
+}
+
+__device__ __forceinline__ void stage_item_gates(const PackedParams& p, const GateBits& g, int wave, int lane,
+                                                 float2* s_gate) {
+  if (wave == 0) {
+    float alpha, beta;
+    ck_gates(decode_act_bits(g.a, p.a_dtype()), decode_act_bits(g.b, p.b_dtype()),
+             decode_act_bits(g.A_log, p.A_log_dtype()), decode_act_bits(g.dt_bias, p.dt_bias_dtype()), &alpha, &beta);
+    if (lane == 0) s_gate[0] = make_float2(alpha, beta);
+  }
+}
+
 template <int WAVES, bool ROTATE>
 __device__ __forceinline__ void stage_gates(const PackedParams& p, const Geom& gm, const WorkSeq& w, int wave,
                                             int lane, float2* s_gate) {
@@ -1003,10 +1033,11 @@ void packed_decode_single_kernel(const int32_t* __restrict__ idx, int items, int
   tl_mark(p, 32);
 #endif
   const int row0 = ca.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g;
+  const GateBits gbits = load_item_gate_bits(p, ca);
   ItemRegs<RPL, L::EW, L::QKT> A;
   load_item<K, RPL, WAVES, RESID, PER_HEAD, ACT>(p, ca, true, row0, c, A);
   tl_mark(p, 33);
-  stage_gates<1, false>(p, gm, WorkSeq{item, 1, 1}, wave, lane, s_gate);  // wave 0: this item's gates
+  stage_item_gates(p, gbits, wave, lane, s_gate);
   tl_mark(p, 34);
   __syncthreads();
   const float2 gab = s_gate[0];

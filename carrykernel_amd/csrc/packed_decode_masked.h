@@ -122,10 +122,10 @@ __global__ __launch_bounds__(WAVES * 64) void packed_decode_masked_kernel(const 
   const Geom gm = geom_of(p);
   const ItemCoord ic = item_coord<false, DST>(p, gm, idx, dst_idx, item);
   const int row0 = ic.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g;
+  const GateBits gbits = load_item_gate_bits(p, ic);  // before the item's loads (see stage_item_gates)
   ItemRegs<RPL, L::EW, L::QKT> R{};
   if (ic.live) load_item_masked<KP, RPL, WAVES, RESID, PER_HEAD, MASK>(p, ic, row0, c, R);
-  // wave 0 evaluates this item's gates into LDS
-  stage_gates<1, false>(p, gm, WorkSeq{item, 1, 1}, wave, lane, s_gate);
+  stage_item_gates(p, gbits, wave, lane, s_gate);  // wave 0 evaluates this item's gates into LDS
   __syncthreads();
   const float2 gab = s_gate[0];
   process_item<KP, RPL, WAVES, RESID, PER_HEAD, MODE, kF32, DST, MASK>(p, ic, row0, c, lane, wave, 0, gab.x, gab.y, R,
