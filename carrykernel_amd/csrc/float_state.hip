@@ -67,7 +67,7 @@ __device__ __forceinline__ void load_fitem(const PackedParams& p, const ItemCoor
       R.sw[i][w] = BF16 ? ld_stream16(sbase + off + 16u * w) : ld_at<u32x4>(sbase, off + 16u * w);
     R.vv[i] = load_act_raw<ESZ>(vbase, r * ESZ);
   }
-  const char* qbase = mrow + (int64_t)(hv / (p.HV / p.H)) * K * ESZ;
+  const char* qbase = mrow + (int64_t)pd::fdiv((uint32_t)hv, p.div_grp) * K * ESZ;
   const uint32_t koff = (uint32_t)((p.H - 1) * K);
 #pragma unroll
   for (int j = 0; j < L::QKT; ++j) {
@@ -322,6 +322,7 @@ extern "C" int ck_gdn_packed_decode_float_state(const void* mixed_qkv, int qkv_d
              (out_dtype << 20);
   p.H = H;
   p.HV = HV;
+  p.div_grp = pd::make_fastdiv((uint32_t)(HV / H));
   p.V = V;
   p.l2norm = use_qk_l2norm ? 1 : 0;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);

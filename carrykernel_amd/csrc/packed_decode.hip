@@ -172,6 +172,7 @@ static int packed_decode_impl(const void* mixed_qkv, int qkv_dtype, int64_t stri
              (out_dtype << 20);
   p.H = H;
   p.HV = HV;
+  p.div_grp = make_fastdiv((uint32_t)(HV / H));
   p.V = V;
   p.K = K;
   p.l2norm = use_qk_l2norm ? 1 : 0;

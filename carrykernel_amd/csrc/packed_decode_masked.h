@@ -89,7 +89,7 @@ __device__ __forceinline__ void load_item_masked(const PackedParams& p, const It
     R.vv[i] = __float_as_uint(decode_act_bits(load_act_bits(p.mixed, vi, adt), adt));
   }
   if constexpr (PER_HEAD) R.es_in[0] = p.rscale[ic.slot * p.stride_rscale + ic.hv];
-  const int64_t head = ic.hv / (p.HV / p.H);
+  const int64_t head = fdiv((uint32_t)ic.hv, p.div_grp);
 #pragma unroll
   for (int j = 0; j < L::QKT; ++j) {
     const int e = min((int)threadIdx.x + j * L::NT, 2 * KP - 1);  // [q | k], each padded to KP
