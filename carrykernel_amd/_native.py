@@ -58,6 +58,7 @@ _SIGNATURES = {
     "ck_last_error": (ctypes.c_char_p, []),
     "ck_abi_version": (_int, []),
     "ck_set_max_items_per_launch": (_int, [_i64]),
+    "ck_set_decode_kernel": (_int, [_int]),
     "ck_gdn_packed_decode": (_int, [
         _vp, _int, _i64,          # mixed_qkv, dtype, stride
         _vp, _int, _i64,          # a
@@ -198,3 +199,17 @@ def set_max_items_per_launch(cap: int) -> None:
     their requests (``ck_set_max_items_per_launch``; used by the tests of the
     split)."""
     check(lib().ck_set_max_items_per_launch(int(cap)), "set_max_items_per_launch")
+
+
+DECODE_KERNEL_AUTO = 0
+DECODE_KERNEL_PERSISTENT = 1
+DECODE_KERNEL_ONE_ITEM = 2
+
+
+def set_decode_kernel(which: int) -> None:
+    """Choose, process-wide, the kernel of the quantized decode steps issued
+    afterwards: DECODE_KERNEL_AUTO (the default), DECODE_KERNEL_PERSISTENT or
+    DECODE_KERNEL_ONE_ITEM for every batch (``ck_set_decode_kernel``; used by
+    the tests to run each kernel on shapes the automatic choice gives to the
+    other). Both give the same bits."""
+    check(lib().ck_set_decode_kernel(int(which)), "set_decode_kernel")

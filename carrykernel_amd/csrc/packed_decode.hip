@@ -44,6 +44,27 @@ int64_t max_items_override() {
   return g_max_items.load(std::memory_order_relaxed);
 }
 
+namespace {
+std::atomic<int> g_decode_kernel{kDecodeKernelAuto};
+std::once_flag g_decode_kernel_env;
+
+// CARRYKERNEL_DECODE_KERNEL (1: persistent, 2: one-item), read on the first
+// launch like CARRYKERNEL_MAX_ITEMS_PER_LAUNCH
+void read_decode_kernel_env() {
+  std::call_once(g_decode_kernel_env, [] {
+    if (const char* e = getenv("CARRYKERNEL_DECODE_KERNEL")) {
+      const int v = atoi(e);
+      if (v == kDecodeKernelPersistent || v == kDecodeKernelOneItem) g_decode_kernel.store(v, std::memory_order_relaxed);
+    }
+  });
+}
+}  // namespace
+
+int decode_kernel_override() {
+  read_decode_kernel_env();
+  return g_decode_kernel.load(std::memory_order_relaxed);
+}
+
 int resident_workgroups(const void* fn, int block, int* per_cu_out) {
   static std::mutex mu;
   struct Entry {
@@ -262,6 +283,15 @@ extern "C" int ck_set_max_items_per_launch(int64_t cap) {
   if (cap < 0) return ck::fail(CK_EINVAL, "the item limit must be >= 0, got %lld", (long long)cap);
   ck::pd::read_max_items_env();  // so that a later first launch does not overwrite it
   ck::pd::g_max_items.store(cap, std::memory_order_relaxed);
+  return ck::ok();
+}
+
+extern "C" int ck_set_decode_kernel(int which) {
+  if (which != ck::pd::kDecodeKernelAuto && which != ck::pd::kDecodeKernelPersistent &&
+      which != ck::pd::kDecodeKernelOneItem)
+    return ck::fail(CK_EINVAL, "the decode kernel must be 0 (automatic), 1 (persistent) or 2 (one-item), got %d", which);
+  ck::pd::read_decode_kernel_env();  // so that a later first launch does not overwrite it
+  ck::pd::g_decode_kernel.store(which, std::memory_order_relaxed);
   return ck::ok();
 }
 

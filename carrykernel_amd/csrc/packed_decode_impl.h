@@ -135,9 +135,11 @@ struct Layout {
 };
 
 // Per-head residual mode keeps every row's unquantized residual until the
-// head's amax is known. With int8 residual rows at 2 rows per lane the 32
-// values go to LDS (each lane reads back only its own) instead of VGPRs, so
-// the 8-wave shape fits 128 VGPRs.
+// head's amax is known. In the persistent kernel, with int8 residual rows at
+// 2 rows per lane, the 32 values go to LDS (each lane reads back only its
+// own) instead of VGPRs, so the 8-wave shape fits 128 VGPRs beside the second
+// register set. The one-item kernel has no second set and keeps them in VGPRs
+// (process_item's EK_REGS).
 template <int RPL, int RESID, bool PER_HEAD>
 constexpr bool kResidInLds = PER_HEAD && RESID == CK_RESID_INT8 && RPL == 2;
 
@@ -399,14 +401,17 @@ __device__ __forceinline__ void store_resid_words(int8_t* dst, const uint32_t (&
 }
 
 // Compute and store one item whose registers are loaded (MASK: see above).
-template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ACT, bool DST, int MASK = kMaskNone>
+// EK_REGS: the per-head residual waits in VGPRs even where kResidInLds would
+// put it in LDS (the one-item kernel).
+template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ACT, bool DST, int MASK = kMaskNone,
+          bool EK_REGS = false>
 __device__ __forceinline__ void process_item(const PackedParams& p, const ItemCoord& ic, int row0, int c, int lane,
                                              int wave, int parity, float alpha, float beta,
                                              const ItemRegs<RPL, Layout<K, RPL, WAVES, RESID, PER_HEAD>::EW,
                                                             Layout<K, RPL, WAVES, RESID, PER_HEAD>::QKT>& R,
                                              float (*s_qk)[2 * K], float (*s_red)[WAVES], float4* s_ek) {
   using L = Layout<K, RPL, WAVES, RESID, PER_HEAD>;
-  constexpr bool EK_LDS = kResidInLds<RPL, RESID, PER_HEAD>;
+  constexpr bool EK_LDS = kResidInLds<RPL, RESID, PER_HEAD> && !EK_REGS;
   constexpr int LPR = L::LPR;
   const int odt = p.out_dtype();
   char* obase = static_cast<char*>(p.out) + ((int64_t)ic.n * p.HV + ic.hv) * p.V * (odt == kF32 ? 4 : 2);
@@ -870,6 +875,14 @@ __device__ __forceinline__ void stage_gates(const PackedParams& p, const Geom& g
   if (v * 64 >= n) __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
 }
 
+// The decode kernel chosen for the process (tests): automatic, or one of the
+// two for every launch (CARRYKERNEL_DECODE_KERNEL, read once, or
+// ck_set_decode_kernel in packed_decode.hip).
+constexpr int kDecodeKernelAuto = 0;
+constexpr int kDecodeKernelPersistent = 1;
+constexpr int kDecodeKernelOneItem = 2;
+int decode_kernel_override();
+
 // A lower limit on the items of one launch set for the process (0: none):
 // CARRYKERNEL_MAX_ITEMS_PER_LAUNCH, read once, or ck_set_max_items_per_launch
 // (packed_decode.hip). Used by the tests of the split.
@@ -1011,9 +1024,11 @@ void packed_decode_kernel(const int32_t* __restrict__ idx, int items, int stride
 //    dispatcher then also balances the end of the launch across CUs (two A/B
 //    pairs on one box, us: per head B=64 28.57 -> 28.15, B=128 48.80 -> 47.24,
 //    B=256 86.49 -> 85.08; per row B=64 28.07 -> 26.81, B=128 47.74 -> 46.49;
-//    per row K=64 B=64 16.03 -> 15.27). Per head at K=32 and 64 it measured
-//    2-3 % slower, and with the int8 residual the head's 64 KB LDS table
-//    keeps it at two workgroups per CU, so those stay persistent.
+//    per row K=64 B=64 16.03 -> 15.27). With the int8 residual per head it
+//    keeps the head's unquantized residual in VGPRs (80, three workgroups per
+//    CU) where the persistent kernel needs a 64 KB LDS table (two): int8 per
+//    head B=64 30.95 -> 28.61, B=256 107.7 -> 101.8 (three A/B pairs). Per
+//    head at K=32 and 64 it measured 2-3 % slower, so those stay persistent.
 // process_item computes the item in both kernels, so the results are the same
 // bits.
 template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ACT, bool DST>
@@ -1026,7 +1041,7 @@ void packed_decode_single_kernel(const int32_t* __restrict__ idx, int items, int
   const Geom gm{items, stride_idx, share_n, shares, FastDiv{nvt_d, nvt_m, nvt_sh}, FastDiv{hv_d, hv_m, hv_sh}, grid};
   __shared__ __attribute__((aligned(16))) float s_qk[4][2 * K];  // [0] staged, [2] raw
   __shared__ float s_red[2][WAVES];
-  __shared__ float4 s_ek[kResidInLds<RPL, RESID, PER_HEAD> ? WAVES * RPL * 4 * 64 : 1];
+  __shared__ float4 s_ek[1];  // unused: the per-head residual waits in VGPRs (EK_REGS)
   __shared__ float2 s_gate[1];
 
   const int lane = threadIdx.x & 63;
@@ -1055,8 +1070,8 @@ void packed_decode_single_kernel(const int32_t* __restrict__ idx, int items, int
   const float2 gab = s_gate[0];
   tl_mark(p, tl_item_slot(0, 0));
   tl_data_ready(p, 0, A);
-  process_item<K, RPL, WAVES, RESID, PER_HEAD, MODE, ACT, DST>(p, ca, row0, c, lane, wave, 0, gab.x, gab.y, A, s_qk,
-                                                              s_red, s_ek);
+  process_item<K, RPL, WAVES, RESID, PER_HEAD, MODE, ACT, DST, kMaskNone, true>(p, ca, row0, c, lane, wave, 0, gab.x,
+                                                                               gab.y, A, s_qk, s_red, s_ek);
   tl_mark(p, tl_item_slot(0, 2));
 }
 
@@ -1088,6 +1103,8 @@ int launch_cfg(PackedParams p, int B, hipStream_t stream) {
                                                                                ACT, DST>);
     single = resident_workgroups(sfn, WAVES * 64, &single_per_cu) > 0 && single_per_cu > per_cu;
   }
+  const int forced = decode_kernel_override();
+  if (forced != kDecodeKernelAuto) single = forced == kDecodeKernelOneItem;
   // the persistent kernel's gate table bounds its items per launch; the
   // one-item kernel has no table, so only a process-wide limit splits it
   const int64_t override_cap = max_items_override();
@@ -1129,10 +1146,11 @@ int launch_cfg(PackedParams p, int B, hipStream_t stream) {
 // HV=32: 6.5 / 6.6 / 7.3 us -> 4.7 / 4.7 / 5.7 us; from B=8 the 64-row tiles
 // are faster). A
 // per-head residual scale needs the whole head in one workgroup; at K=128 that
-// is 8 waves of 2 rows per lane, which fits 128 VGPRs (the int8 residual's
-// unquantized values wait for the head amax in LDS) and so two workgroups per
-// CU; K=64, 32 and 16 spread a 128-row head over more waves (below); other
-// shapes keep 4 rows per lane.
+// is 8 waves of 2 rows per lane: three workgroups per CU in the one-item
+// kernel (80 VGPRs), two in the persistent one (128 VGPRs; the int8
+// residual's unquantized values wait for the head amax in LDS there); K=64,
+// 32 and 16 spread a 128-row head over more waves (below); other shapes keep
+// 4 rows per lane.
 template <int K, int RESID, bool PER_HEAD, int MODE, int ACT, bool DST>
 int launch_k(const PackedParams& p, int B, hipStream_t stream) {
   constexpr int RPI = 64 / (K / 16);

@@ -91,6 +91,19 @@ int ck_abi_version(void);
 int ck_set_max_items_per_launch(int64_t cap);
 
 /*
+ * Choose, for the whole process, which kernel runs the quantized decode
+ * steps issued after it returns: 0 automatic (the default), 1 the persistent
+ * kernel, 2 the one-item kernel, whatever the batch. Both compute every item
+ * with the same code, so the results are the same bits; the automatic choice
+ * is the faster one. It has no counterpart in the reference: it exists so
+ * that the tests run each kernel on shapes the automatic choice gives to the
+ * other. The environment variable CARRYKERNEL_DECODE_KERNEL (1 or 2), read
+ * once at the first launch, sets the same value. Thread-safe. Returns
+ * CK_EINVAL for any other value.
+ */
+int ck_set_decode_kernel(int which);
+
+/*
  * One decode step of the vLLM-layout quantized GDN, updated in place.
  *
  * mixed_qkv [B, 2*H*K + HV*V] (row stride stride_qkv_tok elements, last dim

@@ -20,3 +20,19 @@ def device():
     if not torch.cuda.is_available():
         pytest.skip("no GPU visible")
     return torch.device("cuda", 0)
+
+
+@pytest.fixture
+def decode_kernel(request):
+    """Run the test with the quantized decode's kernel chosen by the test's
+    `decode_kernel` parameter (indirect parametrization: "auto",
+    "persistent" or "one-item"); the automatic choice is restored afterwards,
+    also when the test fails."""
+    from carrykernel_amd import _native
+    which = {"auto": _native.DECODE_KERNEL_AUTO, "persistent": _native.DECODE_KERNEL_PERSISTENT,
+             "one-item": _native.DECODE_KERNEL_ONE_ITEM}[getattr(request, "param", "auto")]
+    _native.set_decode_kernel(which)
+    try:
+        yield which
+    finally:
+        _native.set_decode_kernel(_native.DECODE_KERNEL_AUTO)

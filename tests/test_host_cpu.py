@@ -122,6 +122,10 @@ def test_other_entry_points_argument_errors(L):
     rc = L.ck_set_max_items_per_launch(-1)
     assert rc == _native.CK_EINVAL and "item limit" in L.ck_last_error().decode()
     assert L.ck_set_max_items_per_launch(0) == _native.CK_OK
+    for bad in (-1, 3):
+        rc = L.ck_set_decode_kernel(bad)
+        assert rc == _native.CK_EINVAL and "decode kernel" in L.ck_last_error().decode()
+    assert L.ck_set_decode_kernel(_native.DECODE_KERNEL_AUTO) == _native.CK_OK
     rc = L.ck_quantize_cols(p, 1, 32, 8, 300.0, p, p, None)
     assert rc == _native.CK_EINVAL
     rc = L.ck_gdn_packed_decode_float_state(p, 0, 384, p, 0, 2, p, 0, 2, p, 0, p, 0, 1.0, p, 2, 100, p, 0, p, 1,

@@ -6,10 +6,11 @@ more than one wave) or that the step is split over consecutive launches
 * C3 at B=256 (HV=32, K=V=128, int4 residual with a per-head scale), two
   steps bit for bit against the oracle;
 * B=1100 through the quantized decode (per-head int8 FAST on the
-  persistent kernel: one launch, more than 64 items per workgroup; per-head
-  int4 FAST and per-row int8 EXACT on the one-item kernel: one launch of
-  35,200 / 70,400 workgroups) and through the bf16-state arm (two
-  launches): every item is checked bit for bit;
+  persistent kernel, chosen through ck_set_decode_kernel: one launch, more
+  than 64 items per workgroup; per-head int4 FAST and per-row int8 EXACT on
+  the one-item kernel, the automatic choice: one launch of 35,200 / 70,400
+  workgroups) and through the bf16-state arm (two launches): every item is
+  checked bit for bit;
 * small steps split into launches of a few items (a limit lowered through
   ck_set_max_items_per_launch) with bf16 activations and output,
   strided ids and out-of-place destinations;
@@ -79,17 +80,19 @@ def test_c3_b256_bit_exact(device):
                     False, f"C3 B=256 step {t}")
 
 
-@pytest.mark.parametrize("resid_fmt,per_head,mode", [(oracle.RESID_INT8, True, oracle.MODE_FAST),
-                                                     (oracle.RESID_INT4, True, oracle.MODE_FAST),
-                                                     (oracle.RESID_INT8, False, oracle.MODE_EXACT)])
-def test_more_than_64_items_per_workgroup(device, resid_fmt, per_head, mode):
+@pytest.mark.parametrize("resid_fmt,per_head,mode,decode_kernel", [
+    (oracle.RESID_INT8, True, oracle.MODE_FAST, "persistent"),
+    (oracle.RESID_INT4, True, oracle.MODE_FAST, "auto"),
+    (oracle.RESID_INT8, False, oracle.MODE_EXACT, "auto")], indirect=["decode_kernel"])
+def test_more_than_64_items_per_workgroup(device, resid_fmt, per_head, mode, decode_kernel):
     """B=1100 requests x 32 heads. The int8 per-head step runs the
-    persistent kernel (two workgroups per CU on 256 CUs), which gives every
-    workgroup more than 64 items, so a second wave stages the gates of items
-    64..; the int4 per-head and the per-row int8 steps run the one-item
-    kernel over 35,200 and 70,400 workgroups in one launch (it has no gate
-    table, so no per-launch item limit). GQA (H=16), the in-kernel L2 norm,
-    every item checked bit for bit."""
+    persistent kernel (chosen for the test; two workgroups per CU on 256 CUs
+    with the int8 residual's LDS table), which gives every workgroup more
+    than 64 items, so a second wave stages the gates of items 64..; the int4
+    per-head and the per-row int8 steps run the automatic choice, the
+    one-item kernel, over 35,200 and 70,400 workgroups in one launch (it has
+    no gate table, so no per-launch item limit). GQA (H=16), the in-kernel L2
+    norm, every item checked bit for bit."""
     B = 1100
     S = B + 1
     cus = torch.cuda.get_device_properties(device).multi_processor_count
@@ -105,7 +108,7 @@ def test_more_than_64_items_per_workgroup(device, resid_fmt, per_head, mode):
     torch.cuda.synchronize()
     host = [_host(x) for x in pool]
     out = torch.empty(B, 1, HV, V, device=device)
-    print(f"case B=1100 resid={resid_fmt} per_head={per_head} mode={mode}", flush=True)
+    print(f"case B=1100 resid={resid_fmt} per_head={per_head} mode={mode} kernel={decode_kernel}", flush=True)
     qpd.quantized_gated_delta_rule_packed_decode(
         mixed, a, b, A_log, dt_bias, K ** -0.5, *pool, out, ids, use_qk_l2norm_in_kernel=True,
         resid_fmt=resid_fmt, quant_mode="exact" if mode == oracle.MODE_EXACT else "fast")

@@ -1,11 +1,14 @@
-"""GPU parity of the fused decode where every resident workgroup of the
-persistent grid takes several items (K = V = 128, packed int4 residual, per-
-head or per-row scales, B >= 32 at HV = 32): the item loop's register
-double buffer (item k computed while item k + 1 loads), the alternating LDS
-staging buffers whose parity follows the count of live items, and the
-collapsed prefetch past a workgroup's last item. Each case runs consecutive
-steps on one pool through the drop-in front end and compares the output and
-all four pool tensors bit for bit with the oracle after every step.
+"""GPU parity of the fused decode at batches with several items per resident
+workgroup (K = V = 128, packed int4 residual, per-head or per-row scales,
+B >= 32 at HV = 32), on both kernels: the automatic choice, the one-item
+kernel (one workgroup per item, dispatcher-balanced), and the persistent
+kernel, chosen for the test through ck_set_decode_kernel: its item loop's
+register double buffer (item k computed while item k + 1 loads), the
+alternating LDS staging buffers whose parity follows the count of live
+items, and the collapsed prefetch past a workgroup's last item. Each case
+runs consecutive steps on one pool through the drop-in front end and
+compares the output and all four pool tensors bit for bit with the oracle
+after every step.
 
 Cases cover NULL and out-of-range slots between live items of one workgroup,
 out-of-place destinations, GQA, the in-kernel L2 norm, 16-bit activations
@@ -55,7 +58,8 @@ def _expected_out(o_ref, out_dt):
 
 
 @pytest.mark.parametrize("name", list(CASES))
-def test_multi_item_decode_bit_exact(device, name):
+@pytest.mark.parametrize("decode_kernel", ["auto", "persistent"], indirect=True)
+def test_multi_item_decode_bit_exact(device, name, decode_kernel):
     B, H, per_head, mode, act, out_dt, l2norm, null_frac, bad_id, dst_mode, bits, steps = CASES[name]
     # at least two items per resident workgroup: two 8-wave workgroups per CU
     # with a per-head scale, four 4-wave (64-row tiles) per row
@@ -72,7 +76,7 @@ def test_multi_item_decode_bit_exact(device, name):
     if bad_id:
         src[int(rng.integers(B))] = S + 1
     dst = perm[B:2 * B].copy() if dst_mode else None
-    print(f"case {name}", flush=True)
+    print(f"case {name} kernel={decode_kernel}", flush=True)
     for t in range(steps):
         mixed, a, b, A_log, dt_bias = make_packed_inputs(B, H, HV, K, V, seed=31 * B + t, dtype=act)
         scale = K ** -0.5 if l2norm else 1.0

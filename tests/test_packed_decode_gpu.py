@@ -84,11 +84,13 @@ def test_c3_small_batches_bit_exact(device, B, mode):
 @pytest.mark.parametrize("resid_fmt", [qpd.RESID_INT8, qpd.RESID_INT4])
 @pytest.mark.parametrize("per_head", [False, True])
 @pytest.mark.parametrize("B", [64, 37])
-def test_bit_exact_full_occupancy(device, resid_fmt, per_head, B):
-    """Batches with more items than resident workgroups at K=128: the int8
-    per-head step runs the persistent kernel, whose CU pairs share items
-    unevenly (B=37: pairs with different item counts); the int4 per-head and
-    the per-row steps run the one-item kernel, dispatcher-balanced."""
+@pytest.mark.parametrize("decode_kernel", ["auto", "persistent"], indirect=True)
+def test_bit_exact_full_occupancy(device, resid_fmt, per_head, B, decode_kernel):
+    """Batches with more items than resident workgroups at K=128. The
+    automatic choice runs the one-item kernel, dispatcher-balanced; the
+    persistent kernel, chosen for the test, shares items unevenly between the
+    workgroups of a CU (B=37: CU groups with different item counts) and
+    prefetches each next item into its second register set."""
     _run_both(device, B=B, H=32, HV=32, K=128, V=128, resid_fmt=resid_fmt, per_head=per_head,
               mode="fast", l2norm=False, T=2)
 
@@ -103,18 +105,23 @@ def test_one_item_kernel_at_full_occupancy(device, per_head, mode, act):
               l2norm=True, T=2, seed=7 + per_head, act_dtype=act, out_dtype=act)
 
 
-@pytest.mark.parametrize("K,resid_fmt,mode,act", [
-    (128, qpd.RESID_INT8, "exact", torch.float32),   # int8 per head: its 64 KB LDS table allows two
-    (128, qpd.RESID_INT8, "fast", torch.bfloat16),   # workgroups per CU in either kernel
-    (64, qpd.RESID_INT4, "fast", torch.float32),     # per head below K=128
-    (64, qpd.RESID_INT4, "exact", torch.float16),
-    (256, qpd.RESID_INT4, "fast", torch.float32),
-])
-def test_persistent_kernel_at_full_occupancy(device, K, resid_fmt, mode, act):
-    """Per-head shapes that keep the persistent kernel with more items than
+@pytest.mark.parametrize("K,resid_fmt,mode,act,decode_kernel", [
+    (128, qpd.RESID_INT8, "exact", torch.float32, "persistent"),   # int8 per head: the residual
+    (128, qpd.RESID_INT8, "fast", torch.bfloat16, "persistent"),   # waits in a 64 KB LDS table
+    (128, qpd.RESID_INT8, "fast", torch.float16, "one-item"),      # ... and in VGPRs
+    (64, qpd.RESID_INT4, "fast", torch.float32, "auto"),           # per head below K=128
+    (64, qpd.RESID_INT4, "exact", torch.float16, "auto"),
+    (64, qpd.RESID_INT8, "fast", torch.float32, "auto"),
+    (256, qpd.RESID_INT4, "fast", torch.float32, "auto"),
+], indirect=["decode_kernel"])
+def test_persistent_kernel_at_full_occupancy(device, K, resid_fmt, mode, act, decode_kernel):
+    """Per-head shapes on the persistent kernel with more items than
     resident workgroups (items shared by workgroup age, the next item
-    prefetched into the second register set): HV=32, B=64 (B=32 at K=256,
-    where a 16-wave workgroup holds a CU), the in-kernel L2 norm."""
+    prefetched into the second register set): K = 64 and 256, which the
+    automatic choice keeps there, and K = 128 with the int8 residual, chosen
+    for the test (the automatic choice, the one-item kernel, is the last K=128
+    case); HV=32, B=64 (B=32 at K=256, where a 16-wave workgroup holds a
+    CU), the in-kernel L2 norm."""
     _run_both(device, B=64 if K < 256 else 32, H=32, HV=32, K=K, V=128, resid_fmt=resid_fmt, per_head=True,
               mode=mode, l2norm=True, T=2, seed=K + resid_fmt, act_dtype=act, out_dtype=act)
 
