@@ -252,8 +252,8 @@ __device__ __forceinline__ void load_item(const PackedParams& p, const ItemCoord
     R.vv[i] = load_act_raw<ESZ>(vbase, r * ESZ);
   }
   if constexpr (PER_HEAD) {
-    // one scale per (slot, head), loaded by every lane (a vector load, so it
-    // is ordered with the other prefetches)
+    // one scale per (slot, head) at a uniform address: a scalar load in the
+    // one-item kernel, a vector load in the persistent kernel's item loop
     const float* rsh = p.rscale + slot * p.stride_rscale + hv;
     R.es_in[0] = ld_at<float>(rsh, 0u * (uint32_t)c);
   }
