@@ -924,12 +924,6 @@ constexpr int kMinWavesPerEU = (RPL == 2 && (WAVES == 8 || WAVES == 4)) ? 4 : 1;
 template <int RPL, int WAVES, bool PER_HEAD>
 constexpr int kSingleWavesPerEU = (PER_HEAD && RPL == 2 && WAVES == 8) ? 6 : kMinWavesPerEU<RPL, WAVES>;
 
-// Shapes for which a launch of more items than resident workgroups also takes
-// the one-item kernel when it fits more workgroups per CU (see
-// packed_decode_single_kernel): per head at K=128, per row from K=64.
-template <int K, bool PER_HEAD>
-constexpr bool kSingleForLarge = PER_HEAD ? K == 128 : K >= 64;
-
 template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ACT, bool DST>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(kMinWavesPerEU<RPL, WAVES>)))
 void packed_decode_kernel(const int32_t* __restrict__ idx, int items, int stride_idx, uint32_t nvt_d, uint32_t nvt_m,
@@ -1010,9 +1004,11 @@ void packed_decode_kernel(const int32_t* __restrict__ idx, int items, int stride
 // One item per workgroup: its loads, the gates, the item, with no prefetch of
 // a next item; the grid is one workgroup per item and the hardware dispatcher
 // starts the next one on whichever CU frees a slot. Used (launch_cfg) when a
-// launch has no more items than resident workgroups, and for the shapes where
-// this kernel holds more workgroups per CU than the persistent one does with
-// its second register set (kSingleForLarge).
+// launch has no more items than resident workgroups, and for larger launches
+// when this kernel holds more workgroups per CU than the persistent one does
+// with its second register set, or as many and at least two (a CU then
+// overlaps one workgroup's loads with another's arithmetic without a
+// prefetch).
 //  * Small launches: the persistent loop would issue a past-the-end prefetch
 //    before the item and, at the joins of its conditional stores, wait for
 //    some of those loads; this kernel has no younger loads to wait for
@@ -1027,8 +1023,10 @@ void packed_decode_kernel(const int32_t* __restrict__ idx, int items, int stride
 //    per row K=64 B=64 16.03 -> 15.27). With the int8 residual per head it
 //    keeps the head's unquantized residual in VGPRs (80, three workgroups per
 //    CU) where the persistent kernel needs a 64 KB LDS table (two): int8 per
-//    head B=64 30.95 -> 28.61, B=256 107.7 -> 101.8 (three A/B pairs). Per
-//    head at K=32 and 64 it measured 2-3 % slower, so those stay persistent.
+//    head B=64 30.95 -> 28.61, B=256 107.7 -> 101.8 (three A/B pairs). At
+//    equal occupancy it is faster too, once its start-up chain was shortened
+//    (one box, us: per head K=64 B=256 45.3 -> 42.6, K=32 29.4 -> 26.5, K=16
+//    18.9 -> 16.3; per row K=32 B=256 28.7 -> 25.9, K=16 18.9 -> 16.5).
 // process_item computes the item in both kernels, so the results are the same
 // bits.
 template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ACT, bool DST>
@@ -1094,14 +1092,17 @@ int launch_cfg(PackedParams p, int B, hipStream_t stream) {
   const int resident = resident_workgroups(reinterpret_cast<const void*>(fn), WAVES * 64, &per_cu);
   if (resident <= 0) return fail(CK_ELAUNCH, "cannot query the device occupancy");
   // the one-item kernel (packed_decode_single_kernel): for a launch with no
-  // more items than resident workgroups, and for larger launches of the
-  // kSingleForLarge shapes when it fits more workgroups per CU
+  // more items than resident workgroups, and for a larger one when it fits
+  // more workgroups per CU, or as many and at least two. With one workgroup
+  // per CU the persistent kernel's prefetch is the only overlap of loads and
+  // arithmetic (per head K=256, 16 waves, B=256: 208 against 240 us).
   bool single = items <= resident;
-  if (!single && kSingleForLarge<K, PER_HEAD>) {
+  if (!single) {
     int single_per_cu = 0;
     const void* sfn = reinterpret_cast<const void*>(packed_decode_single_kernel<K, RPL, WAVES, RESID, PER_HEAD, MODE,
                                                                                ACT, DST>);
-    single = resident_workgroups(sfn, WAVES * 64, &single_per_cu) > 0 && single_per_cu > per_cu;
+    single = resident_workgroups(sfn, WAVES * 64, &single_per_cu) > 0 &&
+             (single_per_cu > per_cu || (single_per_cu == per_cu && per_cu >= 2));
   }
   const int forced = decode_kernel_override();
   if (forced != kDecodeKernelAuto) single = forced == kDecodeKernelOneItem;

@@ -108,20 +108,21 @@ def test_one_item_kernel_at_full_occupancy(device, per_head, mode, act):
 @pytest.mark.parametrize("K,resid_fmt,mode,act,decode_kernel", [
     (128, qpd.RESID_INT8, "exact", torch.float32, "persistent"),   # int8 per head: the residual
     (128, qpd.RESID_INT8, "fast", torch.bfloat16, "persistent"),   # waits in a 64 KB LDS table
-    (128, qpd.RESID_INT8, "fast", torch.float16, "one-item"),      # ... and in VGPRs
-    (64, qpd.RESID_INT4, "fast", torch.float32, "auto"),           # per head below K=128
-    (64, qpd.RESID_INT4, "exact", torch.float16, "auto"),
-    (64, qpd.RESID_INT8, "fast", torch.float32, "auto"),
-    (256, qpd.RESID_INT4, "fast", torch.float32, "auto"),
+    (128, qpd.RESID_INT8, "fast", torch.float16, "auto"),          # ... and in VGPRs (one-item)
+    (64, qpd.RESID_INT4, "fast", torch.float32, "persistent"),     # per head below K=128
+    (64, qpd.RESID_INT4, "exact", torch.float16, "persistent"),
+    (64, qpd.RESID_INT8, "fast", torch.float32, "persistent"),
+    (64, qpd.RESID_INT8, "exact", torch.bfloat16, "auto"),
+    (256, qpd.RESID_INT4, "fast", torch.float32, "auto"),          # one 16-wave workgroup per CU
 ], indirect=["decode_kernel"])
 def test_persistent_kernel_at_full_occupancy(device, K, resid_fmt, mode, act, decode_kernel):
-    """Per-head shapes on the persistent kernel with more items than
-    resident workgroups (items shared by workgroup age, the next item
-    prefetched into the second register set): K = 64 and 256, which the
-    automatic choice keeps there, and K = 128 with the int8 residual, chosen
-    for the test (the automatic choice, the one-item kernel, is the last K=128
-    case); HV=32, B=64 (B=32 at K=256, where a 16-wave workgroup holds a
-    CU), the in-kernel L2 norm."""
+    """Per-head shapes with more items than resident workgroups on the
+    persistent kernel (items shared by workgroup age, the next item
+    prefetched into the second register set): K = 256, which the automatic
+    choice keeps there, and K = 64 and 128, chosen for the test (their
+    automatic choice, the one-item kernel, runs the "auto" cases); HV=32,
+    B=64 (B=32 at K=256, where a 16-wave workgroup holds a CU), the in-kernel
+    L2 norm."""
     _run_both(device, B=64 if K < 256 else 32, H=32, HV=32, K=K, V=128, resid_fmt=resid_fmt, per_head=True,
               mode=mode, l2norm=True, T=2, seed=K + resid_fmt, act_dtype=act, out_dtype=act)
 
