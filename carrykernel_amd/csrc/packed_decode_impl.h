@@ -14,15 +14,22 @@
 // stays in VGPRs from load to store: state and residual are read once and
 // written once.
 //
-// Persistence and pipelining. The grid holds as many workgroups as fit on the
-// GPU at once; each loops over items (blockIdx.x, + gridDim.x, ...). While an
-// item is computed, the next item's codes, residual, scales, v and q/k are
-// loading into a second register set, so HBM streams continuously instead of
-// every resident workgroup loading, then computing, in lockstep. Prefetches
-// carry raw bits (activation conversion happens at use), so issuing them never
-// waits. q and k are staged once per item through LDS (double-buffered, one
-// barrier per item). The gates of all of a workgroup's items are evaluated
-// before its item loop, one item per lane, into an LDS table (stage_gates).
+// Two kernels compute items with the same code (process_item), so their bits
+// are the same; launch_cfg picks one per launch.
+//  * One-item kernel (packed_decode_single_kernel): one workgroup per item;
+//    the hardware dispatcher starts the next workgroup on whichever CU frees
+//    a slot, and the two or three workgroups on a CU overlap one's loads with
+//    another's arithmetic. It runs every launch except a per-head K=256 batch
+//    above one item per resident workgroup.
+//  * Persistent kernel (packed_decode_kernel): the grid holds as many
+//    workgroups as fit on the GPU at once; each loops over its items. While
+//    an item is computed, the next item's codes, residual, scales, v and q/k
+//    load into a second register set. The gates of all of a workgroup's items
+//    are evaluated before its item loop, one item per lane, into an LDS table
+//    (stage_gates).
+// Loads carry raw bits (activation conversion happens at use), so issuing them
+// never waits. q and k are staged once per item through LDS (one barrier per
+// item).
 //
 // Arithmetic per row (FAST mode; EXACT differs where ck_quant.h says):
 //   sa = s_in * alpha;  h_j = code_j * sa
