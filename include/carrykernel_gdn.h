@@ -93,7 +93,9 @@ int ck_set_max_items_per_launch(int64_t cap);
 /*
  * Choose, for the whole process, which kernel runs the quantized decode
  * steps issued after it returns: 0 automatic (the default), 1 the persistent
- * kernel, 2 the one-item kernel, whatever the batch. Both compute every item
+ * kernel, 2 the one-item kernel, whatever the batch. It applies to K in
+ * {16, 32, 64, 128, 256} with aligned pools; other K and unaligned pools run
+ * the masked kernel, which has one form only. Both compute every item
  * with the same code, so the results are the same bits; the automatic choice
  * is the faster one. It has no counterpart in the reference: it exists so
  * that the tests run each kernel on shapes the automatic choice gives to the
