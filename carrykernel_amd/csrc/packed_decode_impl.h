@@ -18,7 +18,7 @@
 // are the same; launch_cfg picks one per launch.
 //  * One-item kernel (packed_decode_single_kernel): one workgroup per item;
 //    the hardware dispatcher starts the next workgroup on whichever CU frees
-//    a slot, and the two or three workgroups on a CU overlap one's loads with
+//    a slot, and the workgroups that share a CU overlap one's loads with
 //    another's arithmetic. It runs every launch except a per-head K=256 batch
 //    above one item per resident workgroup.
 //  * Persistent kernel (packed_decode_kernel): the grid holds as many
@@ -836,12 +836,13 @@ constexpr int kWaitVmcnt0 = 0x0f70;  // s_waitcnt simm16: vmcnt 0, expcnt 7, lgk
 // One item's gates into s_gate[0], for the kernels with one item per
 // workgroup: every wave issues the item's four gate-input loads (uniform
 // addresses: scalar loads, which retire independently of the vector loads)
-// before the item's own loads; wave 0 evaluates the gates once those arrive,
+// next to the item's own loads; wave 0 evaluates the gates once those arrive,
 // while the item's bytes are still in flight (graph-replayed, int4 per head,
 // HV=32, us: B=1 5.35 -> 5.09, B=8 6.33 -> 5.82, B=64 25.06 -> 24.58, three
 // A/B pairs), against loading them after the item and evaluating them lane-
-// parallel as stage_gates does. The caller issues its item's loads between
-// the two calls and passes a barrier before reading s_gate[0].
+// parallel as stage_gates does. The caller issues its item's vector loads
+// before stage_item_gates (the one-item kernel issues them before
+// load_item_gate_bits too) and passes a barrier before reading s_gate[0].
 struct GateBits {
   ActBits a, b, A_log, dt_bias;
 };
