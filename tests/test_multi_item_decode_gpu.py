@@ -1,5 +1,5 @@
 """GPU parity of the fused decode at batches with several items per resident
-workgroup (K = V = 128, packed int4 residual, per-head or per-row scales,
+workgroup (K = V = 128, packed int4 or int8 residual, per-head or per-row scales,
 B >= 32 at HV = 32), on both kernels: the automatic choice, the one-item
 kernel (one workgroup per item, dispatcher-balanced), and the persistent
 kernel, chosen for the test through ck_set_decode_kernel: its item loop's
@@ -34,7 +34,7 @@ K = V = 128
 HV = 32
 
 # name: B, H, per_head, mode, act dtype, out dtype, l2norm, NULL fraction,
-#       out-of-range id, out-of-place, state bits, steps
+#       out-of-range id, out-of-place, state bits, steps[, residual format (int4 if absent)]
 CASES = {
     "c3_b64_six_steps": (64, 32, True, "fast", torch.float32, torch.float32, False, 0.0, False, False, 8, 6),
     "nulls_gqa_l2_bf16": (96, 16, True, "fast", torch.bfloat16, torch.bfloat16, True, 0.1, True, False, 8, 3),
@@ -46,6 +46,10 @@ CASES = {
     "per_row_exact_f16": (64, 32, False, "exact", torch.float16, torch.float32, True, 0.0, False, False, 8, 3),
     "per_row_nulls_bf16": (80, 16, False, "fast", torch.bfloat16, torch.bfloat16, False, 0.1, True, False, 8, 2),
     "per_row_out_of_place": (64, 32, False, "fast", torch.float32, torch.float32, True, 0.0, False, True, 8, 2),
+    "int8_head_nulls_exact": (48, 16, True, "exact", torch.float32, torch.float32, True, 0.1, True, False, 8, 2,
+                              qpd.RESID_INT8),
+    "int8_row_out_of_place": (64, 32, False, "fast", torch.bfloat16, torch.bfloat16, False, 0.05, False, True, 8, 2,
+                              qpd.RESID_INT8),
 }
 
 
@@ -60,7 +64,8 @@ def _expected_out(o_ref, out_dt):
 @pytest.mark.parametrize("name", list(CASES))
 @pytest.mark.parametrize("decode_kernel", ["auto", "persistent"], indirect=True)
 def test_multi_item_decode_bit_exact(device, name, decode_kernel):
-    B, H, per_head, mode, act, out_dt, l2norm, null_frac, bad_id, dst_mode, bits, steps = CASES[name]
+    B, H, per_head, mode, act, out_dt, l2norm, null_frac, bad_id, dst_mode, bits, steps = CASES[name][:12]
+    resid_fmt = CASES[name][12] if len(CASES[name]) > 12 else qpd.RESID_INT4
     # at least two items per resident workgroup: two 8-wave workgroups per CU
     # with a per-head scale, four 4-wave (64-row tiles) per row
     cus = torch.cuda.get_device_properties(device).multi_processor_count
@@ -68,7 +73,7 @@ def test_multi_item_decode_bit_exact(device, name, decode_kernel):
     assert items >= 2 * per_cu * cus, f"{name}: batch too small for several items per workgroup"
     rng = np.random.default_rng(zlib.crc32(name.encode()))
     S = 2 * B + 3 if dst_mode else B + 3
-    pool = make_pool(S, HV, V, K, qpd.RESID_INT4, per_head, seed=B, bits=bits)
+    pool = make_pool(S, HV, V, K, resid_fmt, per_head, seed=B, bits=bits)
     dpool = to_dev(pool, device)
     perm = (rng.permutation(S - 1) + 1).astype(np.int32)
     src = perm[:B].copy()
@@ -83,13 +88,13 @@ def test_multi_item_decode_bit_exact(device, name, decode_kernel):
         out = torch.empty(B, 1, HV, V, dtype=out_dt, device=device)
         qpd.quantized_gated_delta_rule_packed_decode(
             mixed.to(device), a.to(device), b.to(device), A_log.to(device), dt_bias.to(device), scale, *dpool, out,
-            torch.from_numpy(src).to(device), use_qk_l2norm_in_kernel=l2norm, resid_fmt=qpd.RESID_INT4,
+            torch.from_numpy(src).to(device), use_qk_l2norm_in_kernel=l2norm, resid_fmt=resid_fmt,
             state_bits=bits, quant_mode=mode,
             dst_state_indices=None if dst is None else torch.from_numpy(dst).to(device))
         torch.cuda.synchronize()
         o_ref = oracle.packed_decode(
             mixed.float().numpy(), a.float().numpy(), b.float().numpy(), A_log.float().numpy(),
-            dt_bias.float().numpy(), scale, *pool, src, H, use_qk_l2norm=l2norm, resid_fmt=qpd.RESID_INT4,
+            dt_bias.float().numpy(), scale, *pool, src, H, use_qk_l2norm=l2norm, resid_fmt=resid_fmt,
             per_head=per_head, state_bits=bits, mode=oracle.MODE_EXACT if mode == "exact" else oracle.MODE_FAST,
             dst_indices=dst)
         np.testing.assert_array_equal(out[:, 0].float().cpu().numpy(), _expected_out(o_ref, out_dt),
