@@ -883,6 +883,20 @@ __device__ __forceinline__ void stage_gates(const PackedParams& p, const Geom& g
   if (v * 64 >= n) __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
 }
 
+// Item of workgroup b in the kernels with one item per workgroup. The
+// dispatcher hands workgroups to the 8 XCDs in turn (b % 8); this bijection of
+// [0, items) gives each XCD one contiguous range of items, so the heads of a
+// request (and the rows of a head's tiles) run on one XCD, against a request's
+// heads spread over all eight in blockIdx order (graph-replayed, int4 per
+// head, HV=32, three A/B pairs, us: B=1 5.00 -> 4.87, B=8 5.83 -> 5.47, B=64
+// 24.02 -> 23.53, B=128 43.1 -> 42.2, B=256 80.4 -> 78.2; per row B=128
+// 41.6 -> 41.4). Any other dispatch order leaves it a permutation of the items.
+__device__ __forceinline__ int xcd_contiguous_item(int b, int items) {
+  const int x = b & 7, j = b >> 3;
+  const int q = items >> 3, r = items & 7;  // XCDs below r take q + 1 items, the others q
+  return x * q + min(x, r) + j;
+}
+
 // The decode kernel chosen for the process (tests): automatic, or one of the
 // two for every launch (CARRYKERNEL_DECODE_KERNEL, read once, or
 // ck_set_decode_kernel in packed_decode.hip).
@@ -1055,7 +1069,7 @@ void packed_decode_single_kernel(const int32_t* __restrict__ idx, int items, int
   const int c = lane % L::LPR;
   const int g = lane / L::LPR;
   tl_start(p);
-  const int item = (int)blockIdx.x;
+  const int item = xcd_contiguous_item((int)blockIdx.x, gm.items);
   const ItemCoord ca = item_coord<false, DST>(p, gm, idx, dst_idx, item);
 #if CK_TIMELINE
   asm volatile("" ::"s"((int)ca.slot));

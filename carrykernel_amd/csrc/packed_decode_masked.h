@@ -118,8 +118,8 @@ __global__ __launch_bounds__(WAVES * 64) void packed_decode_masked_kernel(const 
   const int wave = threadIdx.x >> 6;
   const int c = lane % L::LPR;
   const int g = lane / L::LPR;
-  const int item = (int)blockIdx.x;
   const Geom gm = geom_of(p);
+  const int item = xcd_contiguous_item((int)blockIdx.x, gm.items);
   const ItemCoord ic = item_coord<false, DST>(p, gm, idx, dst_idx, item);
   const int row0 = ic.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g;
   const GateBits gbits = load_item_gate_bits(p, ic);  // before the item's loads (see stage_item_gates)
