@@ -7,12 +7,18 @@ tensors and streams are then valid in the library.
 
 There is no CPU fallback: if the library is missing or no GPU is visible the
 entry points raise ``HipUnavailable`` (a ``RuntimeError``).
+
+Loading the library also loads ``_ck_front`` (``csrc/front.cpp``), the host
+C++ argument checks and launch of the packed decode for its Python front end,
+and binds it to the loaded library's entry points.
 """
 
 from __future__ import annotations
 
 import ctypes
+import importlib.util
 import os
+import sysconfig
 import threading
 
 import torch
@@ -22,6 +28,7 @@ LIB_PATH = os.path.join(PKG_DIR, "lib", "libcarrykernel_gdn.so")
 # measurement build of the same sources with per-workgroup timestamps
 # (CK_TIMELINE); loaded only by use_timeline_build()
 TIMELINE_LIB_PATH = os.path.join(PKG_DIR, "lib", "libcarrykernel_gdn_timeline.so")
+FRONT_PATH = os.path.join(PKG_DIR, "lib", "_ck_front" + sysconfig.get_config_var("EXT_SUFFIX"))
 
 ABI_VERSION = 2
 
@@ -48,6 +55,9 @@ class HipUnavailable(RuntimeError):
 
 _lock = threading.Lock()
 _lib = None
+# _ck_front bound to _lib's packed decode entry points; set with _lib (None
+# until the library is loaded or when the extension is not built)
+_front = None
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -130,8 +140,24 @@ def lib():
                 fn.argtypes = args
             if L.ck_abi_version() != ABI_VERSION:
                 raise HipUnavailable("libcarrykernel_gdn.so ABI version mismatch; rebuild it")
+            _bind_front(L)
             _lib = L
     return _lib
+
+
+def _bind_front(L) -> None:
+    """Load ``_ck_front`` (when built) and give it the addresses of ``L``'s
+    ck_gdn_packed_decode and ck_gdn_packed_decode_to."""
+    global _front
+    if not os.path.exists(FRONT_PATH):
+        _front = None
+        return
+    spec = importlib.util.spec_from_file_location("_ck_front", FRONT_PATH)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    addr = lambda fn: ctypes.cast(fn, ctypes.c_void_p).value
+    mod.bind(addr(L.ck_gdn_packed_decode), addr(L.ck_gdn_packed_decode_to))
+    _front = mod
 
 
 def use_timeline_build():

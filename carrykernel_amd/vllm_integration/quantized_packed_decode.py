@@ -133,12 +133,44 @@ def quantized_gated_delta_rule_packed_decode(
     ``dst_state_indices[n]`` of the same pool; an id outside
     ``[1, num_slots)`` discards the update (``out`` is still written).
     """
+    front = _native._front
+    if front is not None and not _DEBUG:
+        # the usual call: the checks below and the launch, in C++ over the
+        # tensors' metadata (csrc/front.cpp); a call it declines takes the
+        # checks below, which raise the reference's errors
+        try:
+            dev = state_codes.get_device()
+            status = front.DECLINED if dev < 0 else front.packed_decode(
+                mixed_qkv, a, b, A_log, dt_bias, scale, state_codes, state_scale, resid_codes,
+                resid_scale, out, ssm_state_indices, dst_state_indices, use_qk_l2norm_in_kernel,
+                resid_fmt, state_bits, _QUANT_MODES[quant_mode], _native.stream_handle(dev))
+        except Exception:   # an argument of another type: the checks below name it
+            status = front.DECLINED
+        if status != front.DECLINED:
+            _native.check(status, "quantized_gated_delta_rule_packed_decode")
+            return out
+
     if not _native.library_available():
         raise RuntimeError("The HIP library is required for the quantized packed decode "
                            "(build it with `python -m carrykernel_amd.build`)")
+    dev, args = _decode_call_args(mixed_qkv, a, b, A_log, dt_bias, scale, state_codes, state_scale,
+                                  resid_codes, resid_scale, out, ssm_state_indices,
+                                  use_qk_l2norm_in_kernel, resid_fmt, state_bits, quant_mode,
+                                  dst_state_indices)
+    L = _native.lib()
+    fn = L.ck_gdn_packed_decode if dst_state_indices is None else L.ck_gdn_packed_decode_to
+    _native.check(fn(*args, _native.stream_handle(dev)), "quantized_gated_delta_rule_packed_decode")
+    return out
 
-    # validation and messages follow quantized_packed_decode.py:268-309; every
-    # tensor's shape and strides are read once (this runs on every call)
+
+def _decode_call_args(mixed_qkv, a, b, A_log, dt_bias, scale, state_codes, state_scale,
+                      resid_codes, resid_scale, out, ssm_state_indices, use_qk_l2norm_in_kernel,
+                      resid_fmt, state_bits, quant_mode, dst_state_indices, check_devices=True):
+    """The packed decode's checks; returns (device index, the arguments of
+    ck_gdn_packed_decode, or of ck_gdn_packed_decode_to with
+    dst_state_indices, without the stream). ``check_devices=False`` leaves
+    out the device checks (tests on CPU tensors)."""
+    # validation and messages follow quantized_packed_decode.py:268-309
     m_sh, m_st = mixed_qkv.shape, mixed_qkv.stride()
     sc_sh, sc_st = state_codes.shape, state_codes.stride()
     rc_sh = resid_codes.shape
@@ -229,23 +261,23 @@ def quantized_gated_delta_rule_packed_decode(
             raise ValueError(f"dst_state_indices must have at least B={B} entries")
 
     dev = state_codes.get_device()   # -1 for a CPU tensor
-    tensors = (("mixed_qkv", mixed_qkv), ("a", a), ("b", b), ("A_log", A_log),
-               ("dt_bias", dt_bias), ("state_codes", state_codes), ("state_scale", state_scale),
-               ("resid_codes", resid_codes), ("resid_scale", resid_scale), ("out", out),
-               ("ssm_state_indices", ssm_state_indices))
-    if dst_state_indices is not None:
-        tensors += (("dst_state_indices", dst_state_indices),)
-    for name, t in tensors:
-        if t.get_device() != dev or dev < 0:
-            _native.require_gpu(t, name)
-            _native.require_gpu(state_codes, "state_codes")
-            raise ValueError(f"{name} is on {t.device}, the state pool on {state_codes.device}")
+    if check_devices:
+        tensors = (("mixed_qkv", mixed_qkv), ("a", a), ("b", b), ("A_log", A_log),
+                   ("dt_bias", dt_bias), ("state_codes", state_codes), ("state_scale", state_scale),
+                   ("resid_codes", resid_codes), ("resid_scale", resid_scale), ("out", out),
+                   ("ssm_state_indices", ssm_state_indices))
+        if dst_state_indices is not None:
+            tensors += (("dst_state_indices", dst_state_indices),)
+        for name, t in tensors:
+            if t.get_device() != dev or dev < 0:
+                _native.require_gpu(t, name)
+                _native.require_gpu(state_codes, "state_codes")
+                raise ValueError(f"{name} is on {t.device}, the state pool on {state_codes.device}")
     if _DEBUG:
         _check_indices_host(ssm_state_indices[:B], num_slots)
         if dst_state_indices is not None:
             _check_dst_indices_host(ssm_state_indices[:B], dst_state_indices[:B], num_slots)
 
-    L = _native.lib()
     head = (mixed_qkv.data_ptr(), _native.dtype_code(mixed_qkv, "mixed_qkv"), m_st[0],
             a.data_ptr(), _native.dtype_code(a, "a"), a_st[0],
             b.data_ptr(), _native.dtype_code(b, "b"), b_st[0],
@@ -258,17 +290,12 @@ def quantized_gated_delta_rule_packed_decode(
             resid_scale.data_ptr(), rs_st[0],
             out.data_ptr(), _native.dtype_code(out, "out"),
             ssm_state_indices.data_ptr(), ssm_state_indices.stride(0))
+    if dst_state_indices is not None:
+        head += (dst_state_indices.data_ptr(), dst_state_indices.stride(0))
     tail = (num_slots, B, H, HV, K, V,
             int(bool(use_qk_l2norm_in_kernel)), int(resid_fmt), rscale_mode,
-            int(state_bits), _QUANT_MODES[quant_mode],
-            _native.stream_handle(dev))
-    if dst_state_indices is None:
-        status = L.ck_gdn_packed_decode(*head, *tail)
-    else:
-        status = L.ck_gdn_packed_decode_to(*head, dst_state_indices.data_ptr(), dst_state_indices.stride(0),
-                                           *tail)
-    _native.check(status, "quantized_gated_delta_rule_packed_decode")
-    return out
+            int(state_bits), _QUANT_MODES[quant_mode])
+    return dev, head + tail
 
 
 def _check_dst_indices_host(src: torch.Tensor, dst: torch.Tensor, num_slots: int) -> None:
