@@ -76,6 +76,13 @@ __device__ __forceinline__ uint32_t fdiv(uint32_t x, const FastDiv& f) {
   return f.d == 1 ? x : (__umulhi(x, f.m) >> f.sh);
 }
 
+// A FastDiv used for quotients only, in two words: m, and sh with bit 8 set
+// when d == 1 (d itself is then not kept).
+inline uint32_t quotient_word(const FastDiv& f) { return f.sh | (f.d == 1 ? 0x100u : 0u); }
+__device__ __forceinline__ FastDiv quotient_fastdiv(uint32_t m, uint32_t w) {
+  return FastDiv{(w & 0x100u) ? 1u : 0u, m, w & 0xffu};
+}
+
 struct PackedParams {
   const void* mixed;
   const void* a;
@@ -186,6 +193,10 @@ __device__ __forceinline__ Geom geom_of(const PackedParams& p) {
   return Geom{p.items, p.stride_idx, p.cu_share_n, p.cu_shares, p.div_nvt, p.div_hv, (int)gridDim.x};
 }
 
+template <bool DST>
+__device__ __forceinline__ void slot_coord(const PackedParams& p, const Geom& gm, const int32_t* __restrict__ idx,
+                                           const int32_t* __restrict__ dst_idx, ItemCoord& ic);
+
 // Coordinates of an item. `item` is uniform; readfirstlane keeps the results
 // in SGPRs so that the slot id is a scalar load (a vector load here would be
 // ordered behind the prefetch in the vector memory counter).
@@ -202,6 +213,14 @@ __device__ __forceinline__ ItemCoord item_coord(const PackedParams& p, const Geo
   ic.hv = __builtin_amdgcn_readfirstlane((int)(nh - n * gm.hv.d));
   ic.n = __builtin_amdgcn_readfirstlane((int)n);
   ic.vt = __builtin_amdgcn_readfirstlane(ic.vt);
+  slot_coord<DST>(p, gm, idx, dst_idx, ic);
+  return ic;
+}
+
+// The slots of an item whose (n, hv, vt) are set.
+template <bool DST>
+__device__ __forceinline__ void slot_coord(const PackedParams& p, const Geom& gm, const int32_t* __restrict__ idx,
+                                           const int32_t* __restrict__ dst_idx, ItemCoord& ic) {
   ic.slot = (int64_t)idx[(int64_t)ic.n * gm.stride_idx];
   ic.live = ic.slot > 0 && ic.slot < p.num_slots;
   if constexpr (DST) {
@@ -212,7 +231,6 @@ __device__ __forceinline__ ItemCoord item_coord(const PackedParams& p, const Geo
     ic.dslot = ic.slot;
     ic.dlive = ic.live;
   }
-  return ic;
 }
 
 // Issue every load of one item, branch-free: the number of loads is the same
@@ -884,18 +902,49 @@ __device__ __forceinline__ void stage_gates(const PackedParams& p, const Geom& g
 }
 
 // Item of workgroup b in the kernels with one item per workgroup. The
-// dispatcher hands workgroups to the 8 XCDs in turn (b % 8); this bijection of
-// [0, items) gives each XCD one contiguous range of items, so the heads of a
-// request (and the rows of a head's tiles) run on one XCD, against a request's
-// heads spread over all eight in blockIdx order (graph-replayed, int4 per
-// head, HV=32, three A/B pairs, us: B=1 5.00 -> 4.87, B=8 5.83 -> 5.47, B=64
-// 24.02 -> 23.53, B=128 43.1 -> 42.2, B=256 80.4 -> 78.2; per row B=128
-// 41.6 -> 41.4). Any other dispatch order leaves it a permutation of the items.
-__device__ __forceinline__ int xcd_contiguous_item(int b, int items) {
+// dispatcher hands workgroups to the 8 XCDs in turn (b % 8), each XCD with its
+// own L2. This bijection of [0, items) keeps each request's items (its heads
+// and their row tiles) on one XCD, against a request's heads spread over all
+// eight in blockIdx order (graph-replayed, int4 per head, HV=32, three A/B
+// pairs, us: B=1 5.00 -> 4.87, B=8 5.83 -> 5.47, B=64 24.02 -> 23.53, B=128
+// 43.1 -> 42.2, B=256 80.4 -> 78.2). It deals the first 8 * (B / 8) requests
+// to the XCDs in turn, XCD x taking x, x + 8, x + 16, ..., in that order on
+// even XCDs and in reverse on odd ones; the items of the last B % 8 requests
+// are cut into 8 contiguous ranges, one per XCD. Against 8 contiguous ranges
+// of the whole launch (B / 8 requests per XCD), dealing keeps a batch padded
+// at its end with NULL slot ids (a captured batch size) spread over all
+// XCDs, and the reversal keeps the requests running at one time apart in
+// memory (two A/B pairs, us: 24 layers x B=64 with 48 live requests 492 ->
+// 433 per token, all live 548 -> 531; B=64 on consecutive slots 24.6 ->
+// 23.8; random slots B=40 17.06 -> 17.01, B=64 24.36 -> 24.33, B=256 79.07
+// -> 78.85; dealing without the reversal: 440, 539, 24.3, 17.20, 24.52,
+// 79.06). `base` = (B / 8) * items per request, each XCD's workgroups before
+// that tail (0: the whole launch in contiguous ranges). Any other dispatch
+// order leaves it a permutation of the items.
+template <bool DST>
+__device__ __forceinline__ ItemCoord xcd_item_coord(const PackedParams& p, const Geom& gm,
+                                                    const int32_t* __restrict__ idx,
+                                                    const int32_t* __restrict__ dst_idx, int b, int base) {
   const int x = b & 7, j = b >> 3;
-  const int q = items >> 3, r = items & 7;  // XCDs below r take q + 1 items, the others q
-  return x * q + min(x, r) + j;
+  const bool dealt = j < base;  // XCD x's i-th dealt request is request x + 8 i
+  const int tail = gm.items - 8 * base;
+  const int q = tail >> 3, r = tail & 7;  // XCDs below r take q + 1 tail items, the others q
+  // the item's number within the XCD's dealt requests (odd XCDs: from the
+  // last), or within the launch
+  const uint32_t u = dealt ? (uint32_t)((x & 1) ? base - 1 - j : j)
+                           : (uint32_t)(8 * base + x * q + min(x, r) + (j - base));
+  const uint32_t nh = fdiv(u, gm.nvt);
+  const uint32_t i = fdiv(nh, gm.hv);
+  ItemCoord ic;
+  ic.vt = __builtin_amdgcn_readfirstlane((int)(u - nh * gm.nvt.d));
+  ic.hv = __builtin_amdgcn_readfirstlane((int)(nh - i * gm.hv.d));
+  ic.n = __builtin_amdgcn_readfirstlane(dealt ? x + 8 * (int)i : (int)i);
+  slot_coord<DST>(p, gm, idx, dst_idx, ic);
+  return ic;
 }
+
+// (B / 8) * items per request: the `base` of xcd_item_coord.
+inline int xcd_base(int B, int per_request) { return (B >> 3) * per_request; }
 
 // The decode kernel chosen for the process (tests): automatic, or one of the
 // two for every launch (CARRYKERNEL_DECODE_KERNEL, read once, or
@@ -1055,10 +1104,16 @@ template <int K, int RPL, int WAVES, int RESID, bool PER_HEAD, int MODE, int ACT
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(kSingleWavesPerEU<RPL, WAVES, PER_HEAD>)))
 void packed_decode_single_kernel(const int32_t* __restrict__ idx, int items, int stride_idx, uint32_t nvt_d,
                                  uint32_t nvt_m, uint32_t nvt_sh, uint32_t hv_d, uint32_t hv_m, uint32_t hv_sh,
-                                 int share_n, uint32_t shares, int grid, const PackedParams p,
+                                 int xcd_base, uint32_t grp_m, uint32_t grp_w, const PackedParams p_arg,
                                  const int32_t* __restrict__ dst_idx) {
   using L = Layout<K, RPL, WAVES, RESID, PER_HEAD>;
-  const Geom gm{items, stride_idx, share_n, shares, FastDiv{nvt_d, nvt_m, nvt_sh}, FastDiv{hv_d, hv_m, hv_sh}, grid};
+  const Geom gm{items, stride_idx, 0, 0u, FastDiv{nvt_d, nvt_m, nvt_sh}, FastDiv{hv_d, hv_m, hv_sh}, items};
+  // div_grp from two preloaded arguments: the kernel then reads no kernel-
+  // argument dword past l2norm, and no load of the struct's tail (div_grp
+  // and its padding dword, whose register the compiler could reuse for the
+  // item coordinates, making them wait for that load) precedes the slot id
+  PackedParams p = p_arg;
+  p.div_grp = quotient_fastdiv(grp_m, grp_w);
   __shared__ __attribute__((aligned(16))) float s_qk[4][2 * K];  // [0] staged, [2] raw
   __shared__ float s_red[2][WAVES];
   __shared__ float4 s_ek[1];  // unused: the per-head residual waits in VGPRs (EK_REGS)
@@ -1069,8 +1124,7 @@ void packed_decode_single_kernel(const int32_t* __restrict__ idx, int items, int
   const int c = lane % L::LPR;
   const int g = lane / L::LPR;
   tl_start(p);
-  const int item = xcd_contiguous_item((int)blockIdx.x, gm.items);
-  const ItemCoord ca = item_coord<false, DST>(p, gm, idx, dst_idx, item);
+  const ItemCoord ca = xcd_item_coord<DST>(p, gm, idx, dst_idx, (int)blockIdx.x, xcd_base);
 #if CK_TIMELINE
   asm volatile("" ::"s"((int)ca.slot));
   tl_mark(p, 32);
@@ -1146,8 +1200,8 @@ int launch_cfg(PackedParams p, int B, hipStream_t stream) {
   if (single) {
     hipLaunchKernelGGL((packed_decode_single_kernel<K, RPL, WAVES, RESID, PER_HEAD, MODE, ACT, DST>),
                        dim3((unsigned)p.items), dim3(WAVES * 64), 0, stream, p.idx, p.items, p.stride_idx,
-                       p.div_nvt.d, p.div_nvt.m, p.div_nvt.sh, p.div_hv.d, p.div_hv.m, p.div_hv.sh, 0, 0u, p.items,
-                       p, p.dst_idx);
+                       p.div_nvt.d, p.div_nvt.m, p.div_nvt.sh, p.div_hv.d, p.div_hv.m, p.div_hv.sh,
+                       xcd_base(B, p.HV * nvt), p.div_grp.m, quotient_word(p.div_grp), p, p.dst_idx);
     return check_launch("ck_gdn_packed_decode");
   }
   // fewest items per workgroup, then the fewest workgroups achieving it

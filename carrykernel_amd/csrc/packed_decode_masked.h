@@ -119,8 +119,7 @@ __global__ __launch_bounds__(WAVES * 64) void packed_decode_masked_kernel(const 
   const int c = lane % L::LPR;
   const int g = lane / L::LPR;
   const Geom gm = geom_of(p);
-  const int item = xcd_contiguous_item((int)blockIdx.x, gm.items);
-  const ItemCoord ic = item_coord<false, DST>(p, gm, idx, dst_idx, item);
+  const ItemCoord ic = xcd_item_coord<DST>(p, gm, idx, dst_idx, (int)blockIdx.x, gm.share_n);  // share_n: xcd_base
   const int row0 = ic.vt * L::ROWS_WG + wave * L::ROWS_WAVE + g;
   const GateBits gbits = load_item_gate_bits(p, ic);  // before the item's loads (see stage_item_gates)
   ItemRegs<RPL, L::EW, L::QKT> R{};
@@ -142,7 +141,7 @@ int launch_masked_cfg(PackedParams p, int B, hipStream_t stream) {
   p.items = (int)items;
   p.div_nvt = make_fastdiv((uint32_t)nvt);
   p.div_hv = make_fastdiv((uint32_t)p.HV);
-  p.cu_share_n = 0;
+  p.cu_share_n = xcd_base(B, p.HV * nvt);  // the base of xcd_item_coord
   p.cu_shares = 0;
   hipLaunchKernelGGL((packed_decode_masked_kernel<KP, RPL, WAVES, RESID, PER_HEAD, MODE, DST, MASK>), dim3((unsigned)items),
                      dim3(WAVES * 64), 0, stream, p, p.idx, p.dst_idx);
