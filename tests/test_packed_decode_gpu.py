@@ -25,15 +25,20 @@ def _normalize_qk(mixed, B, H, K):
 
 
 def _run_both(device, B, H, HV, K, V, resid_fmt, per_head, mode, l2norm, T=1, seed=0,
-              act_dtype=torch.float32, out_dtype=torch.float32, bits=8, scale=None, normalize_qk=False):
+              act_dtype=torch.float32, out_dtype=torch.float32, bits=8, scale=None, normalize_qk=False,
+              null_tail=0):
     """Run T steps on the GPU and in the oracle from the same pool; assert
-    bit-exact agreement of every output after every step."""
+    bit-exact agreement of every output after every step. The last
+    `null_tail` requests read the NULL block (a batch padded to a captured
+    size)."""
     S = B + 3
     scale = K ** -0.5 if scale is None else scale
     pool = make_pool(S, HV, V, K, resid_fmt, per_head, seed=seed, bits=bits)
     dpool = to_dev(pool, device)
     rng = np.random.default_rng(seed + 1)
     indices = (rng.permutation(S - 1)[:B] + 1).astype(np.int32)
+    if null_tail:
+        indices[B - null_tail:] = qpd.NULL_BLOCK_ID
     didx = torch.from_numpy(indices).to(device)
     for t in range(T):
         mixed, a, b, A_log, dt_bias = make_packed_inputs(B, H, HV, K, V, seed=1000 * seed + t, dtype=act_dtype)
@@ -167,6 +172,20 @@ def test_bit_exact_dtypes(device, act_dtype, out_dtype):
 def test_bit_exact_int6_state(device):
     _run_both(device, B=2, H=32, HV=32, K=128, V=128, resid_fmt=qpd.RESID_INT8, per_head=True,
               mode="fast", l2norm=False, T=3, bits=6, seed=11)
+
+
+@pytest.mark.parametrize("B,null_tail,resid_fmt,per_head", [
+    (64, 16, qpd.RESID_INT4, True),    # whole requests dealt to the XCDs, the NULL ones last
+    (40, 5, qpd.RESID_INT4, True),
+    (45, 9, qpd.RESID_INT8, True),     # dealt requests and a B mod 8 tail in contiguous ranges
+    (21, 6, qpd.RESID_INT4, False),
+])
+def test_padded_batch_bit_exact(device, B, null_tail, resid_fmt, per_head):
+    """A batch padded at its end with NULL slot ids, as a captured batch size
+    is: every live request bit-exact against the oracle, the NULL ones zero,
+    over the one-item kernel's mapping of requests to XCDs."""
+    _run_both(device, B=B, H=16, HV=32, K=128, V=128, resid_fmt=resid_fmt, per_head=per_head, mode="fast",
+              l2norm=True, T=2, seed=23, null_tail=null_tail)
 
 
 def test_null_block_padding(device, H=8, HV=16, K=64, V=64):
